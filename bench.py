@@ -1,0 +1,211 @@
+#!/usr/bin/env python3
+"""PISA-PG sparse attention on one MI355X: ms per attention call and effective TFLOP/s.
+
+A step is one PISA-PG attention call over the workload's synthetic Q/K/V, already
+resident in HBM: K2 (block statistics + phase-2 operand pack), K3 (scores +
+top-k) and K4 (sparse attention with first-order correction).  ``value`` is the
+algorithmic K4 FLOPs divided by the wall-clock time per step (the headline
+"PISA with correction" figure, F / (t_K2 + t_K3 + t_K4)).  The K1 layout
+permutation is timed separately (it is not part of the PASA processors' call).
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--cpu-heads", type=int, default=2, help="heads timed for the CPU baseline")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "PISA shards by head with no communication, so N GPUs run the one-GPU kernels on H/N heads.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from pasa_amd import _lib, ops, placement
+    from pasa_amd.workloads import WORKLOADS, make_inputs
+
+    wl = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    _lib.load()
+    BT, D, H, T = wl.block_size, wl.head_dim, wl.heads, wl.seq_len
+    NT = wl.num_blocks()
+    ns = ops.num_selected(wl.density, NT)
+    flops_k4 = wl.k4_flops(32, ns)
+    scale = wl.op_scale
+
+    log(f"generating {args.workload} inputs: H={H} T={T} D={D} (seed {args.seed})")
+    t0 = time.perf_counter()
+    q, k, v = (t.to(dev) for t in make_inputs(wl, seed=args.seed))
+    torch.cuda.synchronize()
+    log(f"inputs ready in {time.perf_counter() - t0:.1f}s")
+
+    out = torch.empty_like(v)
+    nsteps = args.warmup + args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(nsteps)]
+
+    def step(i):
+        e = evs[i]
+        e[0].record()
+        st = ops.block_stats(q, k, v, BT, 32)
+        pack = ops.pack_phase2(q, st, BT)
+        e[1].record()
+        sel = ops.select_blocks(st, wl.density, scale)
+        e[2].record()
+        ops.sparse_attn_packed(q, k, v, pack, sel, scale, BT, out=out)
+        e[3].record()
+        return sel
+
+    log(f"warmup {args.warmup}")
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for i in range(args.warmup, nsteps):
+        step(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    timed = evs[args.warmup:]
+    k2 = statistics.mean(e[0].elapsed_time(e[1]) for e in timed)
+    k3 = statistics.mean(e[1].elapsed_time(e[2]) for e in timed)
+    k4 = statistics.mean(e[2].elapsed_time(e[3]) for e in timed)
+    k4_med = statistics.median(e[2].elapsed_time(e[3]) for e in timed)
+    achieved = flops_k4 / (k4 * 1e-3) / 1e12
+    value = flops_k4 / (ms_per_step * 1e-3) / 1e12
+    log(f"ms/step {ms_per_step:.3f}  K2+pack {k2:.3f}  K3 {k3:.3f}  K4 {k4:.3f} ms  "
+        f"-> {value:.1f} TFLOP/s effective, K4 {achieved:.1f} TFLOP/s")
+
+    # K1: frame-major <-> token-major permutation of Q, K, V (forward) and O (inverse).
+    F, Hh, W = wl.grid
+    P = Hh * W
+    bufs = [torch.empty_like(t) for t in (q, k, v)]
+    ka, kb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    kc_, kd = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        placement.permute([q, k, v], bufs, F, P, wl.text_tokens)
+        placement.permute([out], [bufs[0]], F, P, wl.text_tokens, inverse=True)
+    reps = 10
+    ka.record()
+    for _ in range(reps):
+        placement.permute([q, k, v], bufs, F, P, wl.text_tokens)
+    kb.record()
+    kc_.record()
+    for _ in range(reps):
+        placement.permute([out], [bufs[0]], F, P, wl.text_tokens, inverse=True)
+    kd.record()
+    torch.cuda.synchronize()
+    k1f = ka.elapsed_time(kb) / reps
+    k1i = kc_.elapsed_time(kd) / reps
+    tensor_bytes = H * T * D * 2
+    k1f_gbps = 2 * 3 * tensor_bytes / (k1f * 1e-3) / 1e9
+    k1i_gbps = 2 * tensor_bytes / (k1i * 1e-3) / 1e9
+    k2_bytes = 3 * tensor_bytes + H * NT * (3 * D + 1) * 4 + H * math.ceil(NT / 32) * D * D * 4
+    log(f"K1 fwd {k1f:.3f} ms ({k1f_gbps:.0f} GB/s)  inv {k1i:.3f} ms ({k1i_gbps:.0f} GB/s)")
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        tj = json.loads(tfile.read_text())
+        traffic = tj.get(f"k4_sparse_attn@{args.workload}", {}).get("bytes_per_launch")
+
+    cpu = None
+    parity = None
+    if not args.no_cpu_baseline:
+        from oracle import pisa_oracle as O
+        h = max(1, min(args.cpu_heads, H))
+        torch.set_num_threads(os.cpu_count() or 1)
+        cores = torch.get_num_threads()
+        log(f"CPU baseline: oracle on {h} of {H} heads, {cores} threads")
+        qc, kc2, vc = make_inputs(wl, seed=args.seed, heads=range(h))
+        t0 = time.perf_counter()
+        ref = O.pisa_pg_attention(qc, kc2, vc, wl.density, BT, 32, scale)
+        cpu_s = time.perf_counter() - t0
+        cpu_tflops = wl.k4_flops(32, ns) * h / H / cpu_s / 1e12
+        cpu = {"value": round(cpu_tflops, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+               "sample": f"{h} of {H} heads of {args.workload}, one fp32 call of the oracle restatement "
+                         f"(oracle/pisa_oracle.py), {cpu_s:.2f} s; ms per full call scaled by H/h = "
+                         f"{cpu_s * 1e3 * H / h:.0f}",
+               "cpu_model": _cpu_model()}
+        m = O.parity_metrics(out[:, :h].cpu(), ref)
+        parity = {"heads": h, "cos": round(m["cos"], 7), "max_abs_over_rms": m["max_abs_over_rms"]}
+        log(f"CPU {cpu_s:.2f}s for {h} heads -> {cpu_tflops:.4f} TFLOP/s; parity {parity}")
+
+    res = {
+        "metric": "ms/attn call + effective TFLOP/s (MFMA util) at Wan-14B 720p shape, 1 GPU",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: {wl.notes}; B=1 H={H} T={T} D={D}, block {BT}, density {wl.density}, "
+                        f"G=32, NS={ns}, NT={NT}; Q pre-scaled by 1/sqrt(128), op scale {scale}",
+            "heads": H, "seq_len": T, "head_dim": D, "block_size": BT, "density": wl.density,
+            "num_selected": ns, "group_size": 32,
+        },
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
+                     "traffic": traffic, "kernel": "k4_sparse_attn", "flops_per_launch": flops_k4},
+        "cpu_baseline": cpu,
+        "stages_ms": {"k2_stats_and_pack": round(k2, 4), "k3_select": round(k3, 4),
+                      "k4_sparse_attn": round(k4, 4), "k4_median": round(k4_med, 4)},
+        "k1_permute": {"fwd_ms": round(k1f, 4), "fwd_GBps": round(k1f_gbps, 1),
+                       "inv_ms": round(k1i, 4), "inv_GBps": round(k1i_gbps, 1),
+                       "frac_of_hbm_peak_fwd": round(k1f_gbps / PEAK_HBM_GBPS, 4)},
+        "k2_GBps_algorithmic": round(k2_bytes / (k2 * 1e-3) / 1e9, 1),
+        "parity_vs_oracle": parity,
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

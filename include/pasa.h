@@ -1,0 +1,175 @@
+/*
+ * pasa.h — C ABI of the MI355X (gfx950) PISA-PG sparse-attention hot path.
+ *
+ * Every entry point is extern "C", takes plain device pointers, sizes and a
+ * hipStream_t passed as void*, and returns an int status (0 = OK, negative =
+ * error, see pasa_status_t).  The library never allocates device memory: the
+ * caller passes every buffer, including workspace.  All shape / dtype / size
+ * checks run on the host before any HIP call, so every error path is reachable
+ * without a GPU.  No entry point synchronises; work is enqueued on `stream`.
+ * No atomics on global memory: identical inputs give bitwise-identical outputs.
+ *
+ * Tensor layout: q, k, v, o are [B, H, T, D] contiguous, passed as BH = B*H
+ * slices of [T, D].  Reference interface cited per entry point; paths are
+ * relative to the reference tree (ZHANGWENTAI/PASA).
+ */
+#ifndef PASA_H_
+#define PASA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PASA_ABI_VERSION 1
+
+typedef enum {
+  PASA_OK = 0,
+  PASA_ERR_NULL_POINTER = -1,   /* a required pointer is NULL                     */
+  PASA_ERR_BAD_SHAPE = -2,      /* a size is <= 0, or sizes are inconsistent      */
+  PASA_ERR_HEAD_DIM = -3,       /* head_dim not in {64, 128}                      */
+  PASA_ERR_BLOCK_SIZE = -4,     /* block_size not in {64, 128}                    */
+  PASA_ERR_NUM_SELECTED = -5,   /* ns outside [1, NT]                             */
+  PASA_ERR_OVERFLOW = -6,       /* an element count overflows the index type     */
+  PASA_ERR_DTYPE = -7,          /* dtype not supported by this entry point        */
+  PASA_ERR_WORKSPACE = -8,      /* workspace NULL or smaller than required        */
+  PASA_ERR_BAD_ARG = -9,        /* scale / density not finite, scale <= 0, ...    */
+  PASA_ERR_TEXT_SEGMENT = -10,  /* text segment does not fit the sequence         */
+  PASA_ERR_LAUNCH = -11,        /* a kernel launch failed (hipGetLastError)       */
+  PASA_ERR_GROUP_SIZE = -12,    /* group_size not supported (GPU path: 32)        */
+  PASA_ERR_TOO_MANY_BLOCKS = -13 /* NT above the select kernel's limit (4096)     */
+} pasa_status_t;
+
+typedef enum {
+  PASA_DTYPE_BF16 = 0,
+  PASA_DTYPE_F16 = 1,
+  PASA_DTYPE_F32 = 2
+} pasa_dtype_t;
+
+/* ---- library / error API ------------------------------------------------ */
+
+/* ABI version of the loaded library (PASA_ABI_VERSION). */
+int pasa_abi_version(void);
+
+/* Static text for a status code. */
+const char* pasa_status_string(int status);
+
+/* Thread-local text of the last error raised on the calling thread ("" if none). */
+const char* pasa_last_error(void);
+
+/* NS = min(max(1, int(density * NT)), NT), the reference's top-k count computed
+ * in double precision with truncation toward zero.
+ * Replaces: svg/kernels/triton/group_pisa_attention.py:373.
+ * Returns NS (>= 1) or a negative status for a non-finite density / NT <= 0. */
+int64_t pasa_num_selected(double density, int64_t num_blocks);
+
+/* ---- K1: frame-major <-> token-major layout permutation -------------------
+ * Forward (inverse = 0), frame-major -> token-major, for sequence row r < S - ctx:
+ *     dst[p*F + f] = src[f*P + p]      (F = num_frame, P = frame_size)
+ * Inverse (inverse = 1), token-major -> frame-major:
+ *     dst[f*P + p] = src[p*F + f]
+ * The last `context_length` rows are copied unchanged.  S = ctx + F*P.
+ * Up to three tensors (Q, K, V) are permuted in one launch; unused src/dst
+ * pointers must be NULL.  head_is_temporal: optional int32 [BH]; a slice whose
+ * flag is 0 is copied unchanged (the reference's "spatial" heads); NULL = all
+ * slices permuted.  dtype selects the element size (2 or 4 bytes); head_dim *
+ * element size must be a multiple of 16 bytes.  src and dst must not overlap.
+ * Replaces: svg/models/hyvideo/placement.py:6-31 (closed forms),
+ *   hunyuan_sparse_head_placement :124-153 (kernel :34-121, forward, 3 tensors),
+ *   hunyuan_hidden_states_placement :360-387 (kernel :285-357, inverse, 1 tensor). */
+int pasa_permute(const void* src0, const void* src1, const void* src2,
+                 void* dst0, void* dst1, void* dst2, int n_tensors,
+                 int64_t bh, int64_t num_frame, int64_t frame_size,
+                 int64_t context_length, int64_t head_dim, int dtype,
+                 const int32_t* head_is_temporal, int inverse, void* stream);
+
+/* ---- K2: block statistics + per-group first-order moment ------------------
+ * For every slice and key block j (NT = ceil(T / block_size), n_j its length):
+ *   qc[j] = mean_t q_t,  kc[j] = mean_t k_t,  vc[j] = sum_t v_t     (fp32 [BH,NT,D])
+ *   hnorm[j] = || sum_t (k_t - kc[j]) v_t^T ||_F                        (fp32 [BH,NT])
+ *   hgroup[g] = (1/G) * sum_{j in group g, j < NT} H_j                 (fp32 [BH,NG,D,D])
+ * with NG = ceil(NT / G).  H_j is never materialised in memory.
+ * Replaces: fused_chunk_reduce group_pisa_attention.py:268-288 (kernel :66-129,
+ *   sqrt at :287) and compute_h_group :291-301. */
+int pasa_block_stats(const void* q, const void* k, const void* v,
+                     float* qc, float* kc, float* vc, float* hnorm, float* hgroup,
+                     int64_t bh, int64_t seq_len, int64_t head_dim,
+                     int64_t block_size, int64_t group_size, int dtype, void* stream);
+
+/* ---- K3: block scores + deterministic top-k -------------------------------
+ * scores[I][j] = sum_d qc[I][d] * (scale * kc[j][d])
+ *              + (use_cov_bias ? log(hnorm[j] + 1e-6) + (noise ? noise[j] : 0) : 0)
+ * idx[I][0..NS) = the NS largest scores of row I, ordered by (score desc, index asc);
+ * ties are broken by lowest index; -0.0 and +0.0 compare equal.
+ * selmask[I][w] bit b set  <=>  key block 32*w + b is in idx[I]   (uint32 [BH,NT,ceil(NT/32)])
+ * NS = pasa_num_selected(density, NT).  noise: optional fp32 [BH, NT] (one draw per
+ * key block, shared by all query blocks; used only with use_cov_bias).  scores_out:
+ * optional fp32 [BH, NT, NT] output; when NULL the workspace holds the scores.
+ * workspace: device buffer of at least pasa_select_workspace_bytes(bh, NT) bytes
+ * (may be NULL when scores_out is given).
+ * Replaces: group_pisa_attention.py:365-375. */
+int pasa_select(const float* qc, const float* kc, const float* hnorm, const float* noise,
+                double scale, double density, int use_cov_bias,
+                int32_t* idx, uint32_t* selmask, float* scores_out,
+                void* workspace, size_t workspace_bytes,
+                int64_t bh, int64_t num_blocks, int64_t head_dim, void* stream);
+
+size_t pasa_select_workspace_bytes(int64_t bh, int64_t num_blocks);
+
+/* Top-k of given fp32 scores [BH, NT, NT] with the rule above: the bit-exact
+ * parity entry of K3 (same kernel as pasa_select's second stage).
+ * Replaces: torch.topk at group_pisa_attention.py:374-375. */
+int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint32_t* selmask,
+                            int64_t bh, int64_t num_blocks, void* stream);
+
+/* ---- K4: block-sparse attention with per-group first-order correction -----
+ * For query block I: exact online-softmax attention over the key blocks idx[I]
+ * (in the order given), then for each group g of 32 key blocks the zero-order
+ * (kc, vc) plus first-order (hgroup) contribution of the blocks of g not in
+ * idx[I], merged into the same running max; o = A / (L + Gamma).
+ * gamma_literal = 1 reproduces the reference exactly: Gamma (the zero-order
+ * denominator, sum p_j * n_j) is not rescaled when the running max rises;
+ * gamma_literal = 0 rescales it with A and L.
+ * scale: the natural-log softmax scale s (> 0); scores use s*log2(e) in base 2
+ * and the first-order term uses s.  Group size is 32 on this path.
+ * workspace: >= pasa_sparse_attn_workspace_bytes(...) bytes (packed bf16 phase-2
+ * operands, written by this call).
+ * Replaces: pisa_pg_fwd_kernel group_pisa_attention.py:135-262, launched at :380-396. */
+int pasa_sparse_attn(const void* q, const void* k, const void* v,
+                     const float* kc, const float* vc, const float* hgroup,
+                     const int32_t* idx, const uint32_t* selmask, void* o,
+                     double scale, int64_t bh, int64_t seq_len, int64_t head_dim,
+                     int64_t block_size, int64_t group_size, int64_t ns,
+                     int gamma_literal, int dtype,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t head_dim,
+                                        int64_t block_size, int64_t group_size);
+
+/* The two halves of pasa_sparse_attn, for callers that reuse the packed phase-2
+ * operands or time the attention kernel alone.
+ * pasa_pack_phase2 writes, per (slice, group of 32 key blocks), kbar, the value
+ * sums (transposed) and Hbar (transposed) as bf16 into `pack`
+ * (pasa_sparse_attn_workspace_bytes(...) bytes).
+ * Replaces: the bf16 stores of kc/vc (group_pisa_attention.py:118-119) and the
+ * bf16 cast of h_group at its use (:251). */
+int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
+                     size_t pack_bytes, int64_t bh, int64_t seq_len, int64_t head_dim,
+                     int64_t block_size, int64_t group_size, void* stream);
+
+/* K4 proper on operands packed by pasa_pack_phase2 (same arguments and semantics
+ * as pasa_sparse_attn otherwise).
+ * Replaces: pisa_pg_fwd_kernel group_pisa_attention.py:135-262. */
+int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack,
+                            size_t pack_bytes, const int32_t* idx, const uint32_t* selmask,
+                            void* o, double scale, int64_t bh, int64_t seq_len,
+                            int64_t head_dim, int64_t block_size, int64_t group_size,
+                            int64_t ns, int gamma_literal, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PASA_H_ */

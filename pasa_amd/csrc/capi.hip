@@ -1,0 +1,303 @@
+// C ABI of the PISA-PG hot path (declared in include/pasa.h).
+//
+// Every entry point validates all arguments on the host before touching the
+// HIP runtime, records a thread-local error message and returns a negative
+// pasa_status_t on failure; kernel launch failures are reported from
+// hipGetLastError as PASA_ERR_LAUNCH.  Nothing here allocates or synchronises.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/pasa.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return PASA_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(PASA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+constexpr int64_t kMaxGridY = 65535;
+constexpr int64_t kMaxI32 = 2147483647;
+
+int check_head_dim(int64_t d) {
+  if (d != 64 && d != 128) return fail(PASA_ERR_HEAD_DIM, "head_dim %lld not in {64, 128}", (long long)d);
+  return PASA_OK;
+}
+
+int check_block(int64_t b) {
+  if (b != 64 && b != 128) return fail(PASA_ERR_BLOCK_SIZE, "block_size %lld not in {64, 128}", (long long)b);
+  return PASA_OK;
+}
+
+int check_bh_seq(int64_t bh, int64_t seq_len, int64_t head_dim) {
+  if (bh <= 0 || seq_len <= 0) return fail(PASA_ERR_BAD_SHAPE, "bh=%lld and seq_len=%lld must be > 0", (long long)bh, (long long)seq_len);
+  if (bh > kMaxGridY) return fail(PASA_ERR_OVERFLOW, "bh=%lld exceeds %lld", (long long)bh, (long long)kMaxGridY);
+  if (seq_len > kMaxI32 / 2) return fail(PASA_ERR_OVERFLOW, "seq_len=%lld too large", (long long)seq_len);
+  if (head_dim > 0 && bh > INT64_MAX / seq_len / head_dim / 4) return fail(PASA_ERR_OVERFLOW, "bh*seq_len*head_dim overflows");
+  return PASA_OK;
+}
+
+// The kernels address one (batch, head) slice through a 32-bit buffer offset;
+// one padded block past the end must still be addressable.
+int check_slice_bytes(int64_t seq_len, int64_t head_dim, int64_t elem_bytes) {
+  if ((seq_len + 128) * head_dim * elem_bytes > (int64_t)UINT32_MAX)
+    return fail(PASA_ERR_OVERFLOW, "seq_len*head_dim*%lld bytes exceeds the 4 GiB slice limit", (long long)elem_bytes);
+  return PASA_OK;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+extern "C" {
+
+int pasa_abi_version(void) { return PASA_ABI_VERSION; }
+
+const char* pasa_status_string(int status) {
+  switch (status) {
+    case PASA_OK: return "ok";
+    case PASA_ERR_NULL_POINTER: return "null pointer";
+    case PASA_ERR_BAD_SHAPE: return "bad shape";
+    case PASA_ERR_HEAD_DIM: return "unsupported head_dim";
+    case PASA_ERR_BLOCK_SIZE: return "unsupported block_size";
+    case PASA_ERR_NUM_SELECTED: return "number of selected blocks out of range";
+    case PASA_ERR_OVERFLOW: return "size overflow";
+    case PASA_ERR_DTYPE: return "unsupported dtype";
+    case PASA_ERR_WORKSPACE: return "workspace missing or too small";
+    case PASA_ERR_BAD_ARG: return "bad argument";
+    case PASA_ERR_TEXT_SEGMENT: return "text segment does not fit";
+    case PASA_ERR_LAUNCH: return "kernel launch failed";
+    case PASA_ERR_GROUP_SIZE: return "unsupported group_size";
+    case PASA_ERR_TOO_MANY_BLOCKS: return "too many key blocks for the select kernel";
+    default: return "unknown status";
+  }
+}
+
+const char* pasa_last_error(void) { return g_err; }
+
+int64_t pasa_num_selected(double density, int64_t num_blocks) {
+  if (num_blocks <= 0) return fail(PASA_ERR_BAD_SHAPE, "num_blocks must be > 0");
+  if (!std::isfinite(density)) return fail(PASA_ERR_BAD_ARG, "density must be finite");
+  const double prod = density * (double)num_blocks;
+  if (!std::isfinite(prod) || std::fabs(prod) > 9.0e18) return fail(PASA_ERR_BAD_ARG, "density * NT overflows");
+  int64_t ns = (int64_t)prod;  // truncation toward zero, as Python's int()
+  if (ns < 1) ns = 1;
+  if (ns > num_blocks) ns = num_blocks;
+  ok();
+  return ns;
+}
+
+int pasa_permute(const void* src0, const void* src1, const void* src2, void* dst0, void* dst1,
+                 void* dst2, int n_tensors, int64_t bh, int64_t num_frame, int64_t frame_size,
+                 int64_t context_length, int64_t head_dim, int dtype,
+                 const int32_t* head_is_temporal, int inverse, void* stream) {
+  if (n_tensors < 1 || n_tensors > 3) return fail(PASA_ERR_BAD_ARG, "n_tensors=%d not in [1, 3]", n_tensors);
+  const void* srcs[3] = {src0, src1, src2};
+  void* dsts[3] = {dst0, dst1, dst2};
+  for (int i = 0; i < n_tensors; ++i)
+    if (!srcs[i] || !dsts[i]) return fail(PASA_ERR_NULL_POINTER, "tensor %d: src/dst is NULL", i);
+  int esize;
+  if (dtype == PASA_DTYPE_BF16 || dtype == PASA_DTYPE_F16) esize = 2;
+  else if (dtype == PASA_DTYPE_F32) esize = 4;
+  else return fail(PASA_ERR_DTYPE, "dtype %d unknown", dtype);
+  if (head_dim <= 0) return fail(PASA_ERR_BAD_SHAPE, "head_dim must be > 0");
+  const int64_t row_bytes = head_dim * esize;
+  if (row_bytes % 16 != 0 || row_bytes > 4096)
+    return fail(PASA_ERR_HEAD_DIM, "head_dim*element size = %lld bytes must be a multiple of 16 and <= 4096", (long long)row_bytes);
+  if (num_frame <= 0 || frame_size <= 0 || context_length < 0)
+    return fail(PASA_ERR_BAD_SHAPE, "num_frame and frame_size must be > 0, context_length >= 0");
+  if (num_frame > kMaxI32 / frame_size) return fail(PASA_ERR_OVERFLOW, "num_frame*frame_size overflows");
+  const int64_t S = context_length + num_frame * frame_size;
+  if (S > kMaxI32) return fail(PASA_ERR_OVERFLOW, "sequence length %lld too large", (long long)S);
+  int rc = check_bh_seq(bh, S, head_dim);
+  if (rc) return rc;
+  if (inverse != 0 && inverse != 1) return fail(PASA_ERR_BAD_ARG, "inverse must be 0 or 1");
+  const uintptr_t bytes = (uintptr_t)(bh * S * row_bytes);
+  for (int i = 0; i < n_tensors; ++i)
+    for (int jx = 0; jx < n_tensors; ++jx) {
+      const uintptr_t a = (uintptr_t)srcs[i], b = (uintptr_t)dsts[jx];
+      if (a < b + bytes && b < a + bytes) return fail(PASA_ERR_BAD_ARG, "src %d overlaps dst %d (in-place permutation is not supported)", i, jx);
+    }
+  return launch_status(pasa::launch_permute(src0, src1, src2, dst0, dst1, dst2, n_tensors, (int)bh, (int)S,
+                                            (int)num_frame, (int)frame_size, (int)context_length,
+                                            (int)row_bytes, head_is_temporal, inverse, (hipStream_t)stream),
+                       "pasa_permute");
+}
+
+int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
+                     float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t head_dim,
+                     int64_t block_size, int64_t group_size, int dtype, void* stream) {
+  if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
+  if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_block_stats: only bf16 inputs are supported");
+  int rc;
+  if ((rc = check_head_dim(head_dim))) return rc;
+  if ((rc = check_block(block_size))) return rc;
+  if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
+  if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
+  if (group_size <= 0 || group_size > 1 << 20) return fail(PASA_ERR_GROUP_SIZE, "group_size %lld must be in [1, 2^20]", (long long)group_size);
+  return launch_status(pasa::launch_block_stats(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh, (int)seq_len,
+                                                (int)head_dim, (int)block_size, (int)group_size,
+                                                (hipStream_t)stream),
+                       "pasa_block_stats");
+}
+
+size_t pasa_select_workspace_bytes(int64_t bh, int64_t num_blocks) {
+  if (bh <= 0 || num_blocks <= 0) return 0;
+  return (size_t)bh * (size_t)num_blocks * (size_t)num_blocks * sizeof(float);
+}
+
+static int check_select_shape(int64_t bh, int64_t nt) {
+  if (bh <= 0 || nt <= 0) return fail(PASA_ERR_BAD_SHAPE, "bh=%lld and num_blocks=%lld must be > 0", (long long)bh, (long long)nt);
+  if (bh > kMaxGridY) return fail(PASA_ERR_OVERFLOW, "bh=%lld exceeds %lld", (long long)bh, (long long)kMaxGridY);
+  if (nt > pasa::kMaxSelectBlocks) return fail(PASA_ERR_TOO_MANY_BLOCKS, "num_blocks=%lld exceeds %d", (long long)nt, pasa::kMaxSelectBlocks);
+  return PASA_OK;
+}
+
+int pasa_select(const float* qc, const float* kc, const float* hnorm, const float* noise,
+                double scale, double density, int use_cov_bias, int32_t* idx, uint32_t* selmask,
+                float* scores_out, void* workspace, size_t workspace_bytes, int64_t bh,
+                int64_t num_blocks, int64_t head_dim, void* stream) {
+  if (!qc || !kc || !idx || !selmask) return fail(PASA_ERR_NULL_POINTER, "pasa_select: NULL pointer");
+  if (use_cov_bias && !hnorm) return fail(PASA_ERR_NULL_POINTER, "pasa_select: hnorm is NULL with use_cov_bias");
+  int rc;
+  if ((rc = check_select_shape(bh, num_blocks))) return rc;
+  if ((rc = check_head_dim(head_dim))) return rc;
+  if (!std::isfinite(scale)) return fail(PASA_ERR_BAD_ARG, "scale must be finite");
+  const int64_t ns = pasa_num_selected(density, num_blocks);
+  if (ns < 0) return (int)ns;
+  float* scores = scores_out;
+  if (!scores) {
+    if (!workspace) return fail(PASA_ERR_WORKSPACE, "pasa_select: need scores_out or a workspace");
+    if (workspace_bytes < pasa_select_workspace_bytes(bh, num_blocks))
+      return fail(PASA_ERR_WORKSPACE, "pasa_select: workspace %zu < %zu bytes", workspace_bytes, pasa_select_workspace_bytes(bh, num_blocks));
+    scores = (float*)workspace;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  rc = launch_status(pasa::launch_scores(qc, kc, hnorm, noise, (float)scale, use_cov_bias, scores, (int)bh,
+                                         (int)num_blocks, (int)head_dim, s),
+                     "pasa_select(scores)");
+  if (rc) return rc;
+  return launch_status(pasa::launch_topk(scores, (int)bh, (int)num_blocks, (int)ns, idx, selmask, s),
+                       "pasa_select(topk)");
+}
+
+int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint32_t* selmask,
+                            int64_t bh, int64_t num_blocks, void* stream) {
+  if (!scores || !idx || !selmask) return fail(PASA_ERR_NULL_POINTER, "pasa_select_from_scores: NULL pointer");
+  int rc;
+  if ((rc = check_select_shape(bh, num_blocks))) return rc;
+  if (ns < 1 || ns > num_blocks) return fail(PASA_ERR_NUM_SELECTED, "ns=%lld not in [1, %lld]", (long long)ns, (long long)num_blocks);
+  return launch_status(pasa::launch_topk(scores, (int)bh, (int)num_blocks, (int)ns, idx, selmask, (hipStream_t)stream),
+                       "pasa_select_from_scores");
+}
+
+size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t head_dim,
+                                        int64_t block_size, int64_t group_size) {
+  if (bh <= 0 || seq_len <= 0 || (head_dim != 64 && head_dim != 128) ||
+      (block_size != 64 && block_size != 128) || group_size != 32)
+    return 0;
+  const int64_t nt = cdiv(seq_len, block_size);
+  const int64_t ng = cdiv(nt, group_size);
+  return (size_t)bh * (size_t)ng * pasa::k4_pack_bytes((int)head_dim, (int)block_size);
+}
+
+static int check_attn_shape(int64_t bh, int64_t seq_len, int64_t head_dim, int64_t block_size,
+                            int64_t group_size) {
+  int rc;
+  if ((rc = check_head_dim(head_dim))) return rc;
+  if ((rc = check_block(block_size))) return rc;
+  if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
+  if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
+  if (group_size != 32) return fail(PASA_ERR_GROUP_SIZE, "group_size %lld != 32", (long long)group_size);
+  if (8 * bh * cdiv(cdiv(seq_len, block_size), 8) > kMaxI32) return fail(PASA_ERR_OVERFLOW, "grid too large");
+  return PASA_OK;
+}
+
+static int check_pack(const void* pack, size_t pack_bytes, int64_t bh, int64_t seq_len, int64_t head_dim,
+                      int64_t block_size, int64_t group_size) {
+  const size_t need = pasa_sparse_attn_workspace_bytes(bh, seq_len, head_dim, block_size, group_size);
+  if (!pack || pack_bytes < need)
+    return fail(PASA_ERR_WORKSPACE, "phase-2 pack buffer %zu < %zu bytes", pack ? pack_bytes : (size_t)0, need);
+  return PASA_OK;
+}
+
+int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack, size_t pack_bytes,
+                     int64_t bh, int64_t seq_len, int64_t head_dim, int64_t block_size,
+                     int64_t group_size, void* stream) {
+  if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_pack_phase2: NULL pointer");
+  int rc;
+  if ((rc = check_attn_shape(bh, seq_len, head_dim, block_size, group_size))) return rc;
+  if ((rc = check_pack(pack, pack_bytes, bh, seq_len, head_dim, block_size, group_size))) return rc;
+  return launch_status(pasa::launch_pack_phase2(kc, vc, hgroup, pack, (int)bh, (int)seq_len, (int)head_dim,
+                                                (int)block_size, (hipStream_t)stream),
+                       "pasa_pack_phase2");
+}
+
+static int check_attn_args(const void* q, const void* k, const void* v, const int32_t* idx,
+                           const uint32_t* selmask, const void* o, double scale, int64_t bh,
+                           int64_t seq_len, int64_t head_dim, int64_t block_size, int64_t group_size,
+                           int64_t ns, int gamma_literal, int dtype) {
+  if (!q || !k || !v || !idx || !selmask || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
+  if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_sparse_attn: only bf16 inputs are supported");
+  int rc;
+  if ((rc = check_attn_shape(bh, seq_len, head_dim, block_size, group_size))) return rc;
+  const int64_t nt = cdiv(seq_len, block_size);
+  if (ns < 1 || ns > nt) return fail(PASA_ERR_NUM_SELECTED, "ns=%lld not in [1, %lld]", (long long)ns, (long long)nt);
+  if (nt > INT64_MAX / bh / ns) return fail(PASA_ERR_OVERFLOW, "bh*NT*ns overflows");
+  if (!std::isfinite(scale) || !(scale > 0.0)) return fail(PASA_ERR_BAD_ARG, "scale must be finite and > 0");
+  if (gamma_literal != 0 && gamma_literal != 1) return fail(PASA_ERR_BAD_ARG, "gamma_literal must be 0 or 1");
+  return PASA_OK;
+}
+
+int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack, size_t pack_bytes,
+                            const int32_t* idx, const uint32_t* selmask, void* o, double scale, int64_t bh,
+                            int64_t seq_len, int64_t head_dim, int64_t block_size, int64_t group_size,
+                            int64_t ns, int gamma_literal, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, head_dim, block_size, group_size,
+                            ns, gamma_literal, dtype)))
+    return rc;
+  if ((rc = check_pack(pack, pack_bytes, bh, seq_len, head_dim, block_size, group_size))) return rc;
+  return launch_status(pasa::launch_sparse_attn(q, k, v, pack, idx, selmask, o, (float)scale, (int)bh,
+                                                (int)seq_len, (int)head_dim, (int)block_size, (int)ns,
+                                                gamma_literal, (hipStream_t)stream),
+                       "pasa_sparse_attn");
+}
+
+int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* kc, const float* vc,
+                     const float* hgroup, const int32_t* idx, const uint32_t* selmask, void* o,
+                     double scale, int64_t bh, int64_t seq_len, int64_t head_dim, int64_t block_size,
+                     int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
+  int rc;
+  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, head_dim, block_size, group_size,
+                            ns, gamma_literal, dtype)))
+    return rc;
+  if ((rc = check_pack(workspace, workspace_bytes, bh, seq_len, head_dim, block_size, group_size))) return rc;
+  if ((rc = pasa_pack_phase2(kc, vc, hgroup, workspace, workspace_bytes, bh, seq_len, head_dim, block_size,
+                             group_size, stream)))
+    return rc;
+  return pasa_sparse_attn_packed(q, k, v, workspace, workspace_bytes, idx, selmask, o, scale, bh, seq_len,
+                                 head_dim, block_size, group_size, ns, gamma_literal, dtype, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,139 @@
+// Shared device-side definitions for the gfx950 PISA-PG kernels.
+//
+// Layout conventions used by K2 and K4:
+//  * 16-byte "chunks": 8 bf16 values.  LDS tiles use PadTile (padded rows,
+//    even-first chunk order), which keeps the MFMA operand reads of 16
+//    consecutive rows conflict-free and makes a lane's successive k-step reads
+//    immediate offsets from one base address.
+//  * Transposed tiles ([feature][token]) additionally permute tokens inside
+//    each 16-token group (tok_perm), so that the 8 tokens one lane feeds to a
+//    32x32x16 MFMA as its A-operand slots are one contiguous 16-byte chunk.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pasa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---- bf16 helpers ---------------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet); returns the 16 bits.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  __bf16 b = (__bf16)f;
+  return (uint32_t)__builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// Unpack one 16-byte chunk of 8 bf16 into fp32.
+__device__ __forceinline__ void unpack8(const uint4& c, float* out) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& c) {
+  return __builtin_bit_cast(bf16x8_t, c);
+}
+
+// ---- buffer loads ------------------------------------------------------------
+// A raw buffer resource over [base, base + bytes): loads whose byte range lies
+// beyond `bytes` return zeros in hardware, which pads ragged last blocks
+// without branches.  Offsets are 32-bit, so one resource covers one slice.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t byte_off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+// ---- LDS tile layouts -----------------------------------------------------
+
+// Padded tile of bf16 rows with COLS columns.  Row stride is COLS*2 + 16 bytes,
+// so 16 consecutive rows start on 16 distinct 16-byte bank groups, and the
+// 16-byte chunks of a row are stored even-first (chunk c at position
+// (c & 1) * COLS/16 + c/2).  A half-wavefront (h = lane / 32) reads chunks
+// h, h+2, h+4, ... over consecutive MFMA k-steps, which are therefore
+// contiguous: lane base + 16 * ks, an immediate offset.
+template <int COLS>
+struct PadTile {
+  static constexpr int ROW_BYTES = COLS * 2 + 16;
+  static constexpr int HALF = COLS / 16;
+  __host__ __device__ static constexpr int chunk_pos(int c) { return (c & 1) * HALF + (c >> 1); }
+  __host__ __device__ static constexpr int chunk_byte(int row, int c) {
+    return row * ROW_BYTES + chunk_pos(c) * 16;
+  }
+  __host__ __device__ static constexpr int elem_byte(int row, int col) {
+    return chunk_byte(row, col >> 3) + (col & 7) * 2;
+  }
+  // Byte offset of the k-step-0 chunk a lane of half h reads from `row`.
+  __host__ __device__ static constexpr int frag_base(int row, int h) {
+    return row * ROW_BYTES + h * HALF * 16;
+  }
+  static constexpr int bytes(int rows) { return rows * ROW_BYTES; }
+};
+
+// Token permutation inside each 16-token group: swap bits 2 and 3.  Applied to
+// the token axis of transposed tiles ([feature][token]) so that the 8 tokens a
+// lane feeds to one 32x32x16 MFMA as its A-operand slots (tokens
+// 16s + 4h + {0..3} and 16s + 8 + 4h + {0..3}) form one 16-byte chunk.
+__host__ __device__ __forceinline__ constexpr int tok_perm(int t) {
+  return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1);
+}
+
+template <typename T>
+__device__ __forceinline__ T lds_ld(const unsigned char* base, int byte_off) {
+  return *reinterpret_cast<const T*>(base + byte_off);
+}
+template <typename T>
+__device__ __forceinline__ void lds_st(unsigned char* base, int byte_off, const T& v) {
+  *reinterpret_cast<T*>(base + byte_off) = v;
+}
+
+// ---- MFMA -----------------------------------------------------------------
+
+// D(32x32, fp32) += A(32x16) * B(16x32), bf16 inputs.
+// A: lane l holds A[l%32][8*(l/32) .. +7]; B: lane l holds B[8*(l/32) .. +7][l%32];
+// D: lane l, element r holds D[8*(r/4) + 4*(l/32) + r%4][l%32].
+__device__ __forceinline__ f32x16_t mfma32(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row of the 32x32 D tile held by element r of a lane in half h (= lane / 32).
+__device__ __forceinline__ int mfma32_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// ---- wave helpers -----------------------------------------------------------
+
+__device__ __forceinline__ float xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace pasa

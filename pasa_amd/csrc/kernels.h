@@ -1,0 +1,38 @@
+// Internal launcher declarations (host side).  Shapes are validated by capi.hip
+// before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pasa {
+
+constexpr int kMaxSelectBlocks = 4096;  // NT limit of the top-k kernel (LDS-resident row)
+
+hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* d0, void* d1,
+                          void* d2, int ntens, int bh, int S, int F, int P, int ctx, int row_bytes,
+                          const int32_t* head_is_temporal, int inverse, hipStream_t stream);
+
+hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
+                              float* vc, float* hnorm, float* hgroup, int bh, int T, int D, int BT,
+                              int G, hipStream_t stream);
+
+hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,
+                         float scale, int use_cov_bias, float* scores, int bh, int NT, int D,
+                         hipStream_t stream);
+
+hipError_t launch_topk(const float* scores, int bh, int NT, int NS, int32_t* idx,
+                       uint32_t* selmask, hipStream_t stream);
+
+size_t k4_pack_bytes(int D, int BT);  // per (slice, group) phase-2 pack image
+
+hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
+                              int bh, int T, int D, int BT, hipStream_t stream);
+
+hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
+                              const int32_t* idx, const uint32_t* selmask, void* o, float scale,
+                              int bh, int T, int D, int BT, int NS, int gamma_literal,
+                              hipStream_t stream);
+
+}  // namespace pasa

@@ -1,0 +1,446 @@
+// K4: block-sparse flash attention with per-group first-order correction.
+//
+// Reference: pisa_pg_fwd_kernel, svg/kernels/triton/group_pisa_attention.py:135-262
+//   Phase 1 (:170-186): exact online softmax (base 2) over the selected key
+//     blocks, in top-k order; columns >= T masked.
+//   Phase 2 (:212-253): per group g of 32 key blocks, the blocks not selected
+//     contribute p_j (V^_j + s * Hbar_g^T q) with p_j = 2^(c q.kbar_j - m);
+//     A and L are rescaled when the running max rises, Gamma = sum p_j n_j is
+//     not (the reference's literal form, :201/:243; gamma_literal = 0 gives the
+//     rescaled "consistent" form).
+//   Finalize (:258-262): o = A / (L + Gamma).
+//
+// MI355X mapping.  One workgroup = one (slice, query block) of BT rows; one
+// wavefront per 32 query rows.  Everything is computed transposed so that a lane
+// owns one query (lane % 32) and the softmax statistics are per-lane scalars:
+//   S^T[key][q]  = K  * Q^T   (v_mfma_f32_32x32x16_bf16, K from LDS, Q in VGPRs)
+//   O^T[e][q]   += V^T * P^T   (V^T from LDS, P from the S^T accumulators)
+// The S^T accumulator of a lane already holds, per 16-key step s, exactly the 8
+// keys (16s + 8i' + 4h + j) that the lane's P^T B-operand slots need; V^T is
+// written to LDS with tokens permuted by tok_perm so the matching A-operand
+// slots are one 16-byte LDS read.  Keys of a block are consumed in halves of
+// 64 (one online-softmax step each) to bound live accumulators.
+// The K/V tiles of block i+1 are fetched into registers while block i computes.
+// Workgroups are mapped XCD-aware: each XCD walks a contiguous run of query
+// blocks of the same head, so neighbouring query blocks (whose selections
+// overlap) share that XCD's L2.
+//
+// Phase-2 operands (kbar, V^ transposed, Hbar transposed; bf16) are packed per
+// (slice, group) by k4_pack into the exact LDS image K4 copies in.
+#include "common.h"
+#include "kernels.h"
+
+namespace pasa {
+
+constexpr int kGroup = 32;
+
+template <int D, int BT>
+struct K4Cfg {
+  static constexpr int WAVES = BT / 32;
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int CH = D / 8;
+  using KT = PadTile<D>;       // K tile:        BT rows x D
+  using VT = PadTile<BT>;      // V^T tile:      D rows x BT tokens (tok_perm order)
+  using PKB = PadTile<D>;      // kbar:          32 rows x D
+  using PVT = PadTile<kGroup>; // V^ transposed: D rows x 32 means (tok_perm order)
+  using PHT = PadTile<D>;      // Hbar^T:        D rows (e) x D (d)
+  static constexpr int KS_BYTES = KT::bytes(BT);
+  static constexpr int P1_BYTES = KS_BYTES + VT::bytes(D);
+  static constexpr int PK_VT_OFF = PKB::bytes(kGroup);
+  static constexpr int PK_HT_OFF = PK_VT_OFF + PVT::bytes(D);
+  static constexpr int PK_RAW = PK_HT_OFF + PHT::bytes(D);
+  static constexpr int PK_BYTES = (PK_RAW + 16 * THREADS - 1) / (16 * THREADS) * (16 * THREADS);
+  static constexpr int LDS_BYTES = P1_BYTES > PK_BYTES ? P1_BYTES : PK_BYTES;
+  static constexpr int K_LOADS = (BT * D / 8) / THREADS;   // 16-byte K chunks per thread
+  static constexpr int V_UNITS = (BT * D / 16) / THREADS;  // (2 rows x 16 bytes) V units per thread
+  static constexpr int PK_LOADS = PK_BYTES / 16 / THREADS;
+  static_assert(K_LOADS * THREADS * 8 == BT * D, "K tile split");
+  static_assert(V_UNITS * THREADS * 16 == BT * D, "V tile split");
+  static_assert(THREADS % CH == 0, "K rows per pass");
+};
+
+size_t k4_pack_bytes(int D, int BT) {
+  if (D == 128 && BT == 128) return K4Cfg<128, 128>::PK_BYTES;
+  if (D == 128 && BT == 64) return K4Cfg<128, 64>::PK_BYTES;
+  if (D == 64 && BT == 128) return K4Cfg<64, 128>::PK_BYTES;
+  if (D == 64 && BT == 64) return K4Cfg<64, 64>::PK_BYTES;
+  return 0;
+}
+
+// ---- phase-2 operand pack ---------------------------------------------------
+
+template <int D, int BT>
+__global__ __launch_bounds__(256) void k4_pack(const float* __restrict__ kc,
+                                               const float* __restrict__ vc,
+                                               const float* __restrict__ hgroup,
+                                               unsigned char* __restrict__ pack, int NT, int NG) {
+  using C = K4Cfg<D, BT>;
+  const int g = blockIdx.x;
+  const int bh = blockIdx.y;
+  unsigned char* out = pack + ((int64_t)bh * NG + g) * C::PK_BYTES;
+  const float* kb = kc + (int64_t)bh * NT * D;
+  const float* vb = vc + (int64_t)bh * NT * D;
+  const float* hb = hgroup + ((int64_t)bh * NG + g) * D * D;
+  for (int u = threadIdx.x; u < kGroup * D; u += 256) {
+    const int m = u / D;
+    const int d = u - m * D;
+    const int jj = g * kGroup + m;
+    const float x = jj < NT ? kb[(int64_t)jj * D + d] : 0.f;
+    *(uint16_t*)(out + C::PKB::elem_byte(m, d)) = (uint16_t)f32_to_bf16_bits(x);
+  }
+  for (int u = threadIdx.x; u < D * kGroup; u += 256) {
+    const int m = u % kGroup;
+    const int e = u / kGroup;
+    const int jj = g * kGroup + m;
+    const float x = jj < NT ? vb[(int64_t)jj * D + e] : 0.f;
+    *(uint16_t*)(out + C::PK_VT_OFF + C::PVT::elem_byte(e, tok_perm(m))) =
+        (uint16_t)f32_to_bf16_bits(x);
+  }
+  for (int u = threadIdx.x; u < D * D; u += 256) {
+    const int d = u / D;  // Hbar[d][e] row-major in, Hbar^T[e][d] out
+    const int e = u - d * D;
+    *(uint16_t*)(out + C::PK_HT_OFF + C::PHT::elem_byte(e, d)) = (uint16_t)f32_to_bf16_bits(hb[u]);
+  }
+}
+
+// ---- main kernel ------------------------------------------------------------
+
+template <int D, int BT>
+__global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
+void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                    const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
+                    const int32_t* __restrict__ idx, const uint32_t* __restrict__ selmask,
+                    uint16_t* __restrict__ o, float scale, float c, int T, int NT, int NS,
+                    int NG, int NW, int xcd_chunk, int gamma_literal) {
+  using C = K4Cfg<D, BT>;
+  using KT = typename C::KT;
+  using VT = typename C::VT;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[C::LDS_BYTES];
+  unsigned char* Ks = lds;
+  unsigned char* Vt = lds + C::KS_BYTES;
+
+  // XCD-aware workgroup -> (slice, query block) map: consecutive workgroup ids
+  // go to consecutive XCDs, so slot = wg / 8 indexes within one XCD's run.
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7;
+  const int slot = wg >> 3;
+  const int bh = slot / xcd_chunk;
+  const int qb = xcd * xcd_chunk + (slot - bh * xcd_chunk);
+  if (qb >= NT) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+  const int64_t slice = (int64_t)bh * T * D;
+  const int qrow = qb * BT + wave * 32 + l32;  // the query this lane owns
+
+  const uint32_t slice_bytes = (uint32_t)T * D * 2u;
+  const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
+  const rsrc_t kr = make_rsrc(k + slice, slice_bytes);
+  const rsrc_t vr = make_rsrc(v + slice, slice_bytes);
+
+  // Q fragments (B operand of S^T and of r^T): lane holds Q[qrow][16ks + 8h .. +7].
+  bf16x8_t qf[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    qf[ks] = as_bf16x8(buf_load16(qr, ((uint32_t)qrow * D + ks * 16 + h * 8) * 2u));
+
+  f32x16_t oacc[D / 32];
+#pragma unroll
+  for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[et][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  float g_run = 0.f;
+
+  const int32_t* irow = idx + ((int64_t)bh * NT + qb) * NS;
+
+  // Lane-constant parts of the tile load / store addresses.
+  constexpr int KROWS = C::THREADS / C::CH;  // K rows covered per load pass
+  const uint32_t k_goff = (uint32_t)((tid / C::CH) * D + (tid % C::CH) * 8) * 2u;
+  const int k_soff = KT::chunk_byte(tid / C::CH, tid % C::CH);
+  const int vp = 16 * wave + (lane & 15);  // key pair (2vp, 2vp+1) this lane moves
+  const uint32_t v_goff = (uint32_t)(2 * vp * D + (lane >> 4) * 8) * 2u;
+  const int v_soff = VT::elem_byte(8 * (lane >> 4), tok_perm(2 * vp));
+  const int ka_base = KT::frag_base(l32, h);
+  const int va_base = VT::frag_base(l32, h);
+
+  // ---------------- Phase 1: exact attention over the selected blocks --------
+  uint4 kreg[C::K_LOADS];
+  uint4 vreg[C::V_UNITS][2];
+  auto fetch = [&](int blk) {
+    const uint32_t base = (uint32_t)blk * BT * D * 2u;
+#pragma unroll
+    for (int it = 0; it < C::K_LOADS; ++it)
+      kreg[it] = buf_load16(kr, base + k_goff + it * KROWS * D * 2);
+#pragma unroll
+    for (int it = 0; it < C::V_UNITS; ++it)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) vreg[it][s] = buf_load16(vr, base + v_goff + it * 64 + s * D * 2);
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int it = 0; it < C::K_LOADS; ++it) lds_st(Ks, k_soff + it * KROWS * KT::ROW_BYTES, kreg[it]);
+#pragma unroll
+    for (int it = 0; it < C::V_UNITS; ++it) {
+      const uint32_t a[4] = {vreg[it][0].x, vreg[it][0].y, vreg[it][0].z, vreg[it][0].w};
+      const uint32_t b[4] = {vreg[it][1].x, vreg[it][1].y, vreg[it][1].z, vreg[it][1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t lo = (i & 1) ? (a[i >> 1] >> 16) : (a[i >> 1] & 0xffffu);
+        const uint32_t hi = (i & 1) ? (b[i >> 1] & 0xffff0000u) : (b[i >> 1] << 16);
+        lds_st(Vt, v_soff + (32 * it + i) * VT::ROW_BYTES, lo | hi);
+      }
+    }
+  };
+
+  fetch(irow[0]);
+  for (int it = 0; it < NS; ++it) {
+    const int blk = irow[it];
+    __syncthreads();
+    stash();
+    __syncthreads();
+    if (it + 1 < NS) fetch(irow[it + 1]);
+
+    const int nvalid = min(BT, T - blk * BT);
+#pragma unroll
+    for (int kh = 0; kh < BT / 64; ++kh) {
+      f32x16_t sacc[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[mt][r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const bf16x8_t a = as_bf16x8(
+              lds_ld<uint4>(Ks, ka_base + (kh * 64 + mt * 32) * KT::ROW_BYTES + ks * 16));
+          sacc[mt] = mfma32(a, qf[ks], sacc[mt]);
+        }
+      if (nvalid < BT) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (kh * 64 + mt * 32 + mfma32_row(r, h) >= nvalid) sacc[mt][r] = -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[mt][r]);
+      mx = fmaxf(mx, xor32(mx));
+      // A fully masked half (only in a ragged last block) leaves the state unchanged.
+      const float m_new = fmaxf(m_run, mx * c);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      float psum = 0.f;
+      bf16x8_t pf[4];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p0 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i], c, -m_new));
+          const float p1 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i + 1], c, -m_new));
+          psum += p0 + p1;
+          w[i] = pack_bf16x2(p0, p1);
+        }
+        pf[s4] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+      }
+      m_run = m_new;
+      l_run = l_run * alpha + psum;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int et = 0; et < D / 32; ++et) {
+          const bf16x8_t a = as_bf16x8(
+              lds_ld<uint4>(Vt, va_base + et * 32 * VT::ROW_BYTES + (kh * 4 + s4) * 16));
+          oacc[et] = mfma32(a, pf[s4], oacc[et]);
+        }
+    }
+  }
+
+  // ---------------- Phase 2: zero- + first-order correction per group --------
+  using PKB = typename C::PKB;
+  using PVT = typename C::PVT;
+  using PHT = typename C::PHT;
+  const unsigned char* Pkb = lds;
+  const unsigned char* Pvt = lds + C::PK_VT_OFF;
+  const unsigned char* Pht = lds + C::PK_HT_OFF;
+  const int kb_base = PKB::frag_base(l32, h);
+  const int pv_base = PVT::frag_base(l32, h);
+  const int ph_base = PHT::frag_base(l32, h);
+  const int last_len = T - (NT - 1) * BT;
+  const uint32_t* mrow = selmask + ((int64_t)bh * NT + qb) * NW;
+  for (int g = 0; g < NG; ++g) {
+    // Blocks of this group that take the approximation (uniform over the workgroup).
+    const int nin = min(kGroup, NT - g * kGroup);
+    const uint32_t inrange = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+    const uint32_t approx = inrange & ~mrow[g];
+    if (approx == 0u) continue;  // every block exact or absent: no contribution
+
+    __syncthreads();
+    {
+      const uint4* src = (const uint4*)(pack + ((int64_t)bh * NG + g) * C::PK_BYTES);
+      uint4 preg[C::PK_LOADS];
+#pragma unroll
+      for (int i = 0; i < C::PK_LOADS; ++i) preg[i] = src[i * C::THREADS + tid];
+#pragma unroll
+      for (int i = 0; i < C::PK_LOADS; ++i) ((uint4*)lds)[i * C::THREADS + tid] = preg[i];
+    }
+    __syncthreads();
+
+    f32x16_t sb;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sb[r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Pkb, kb_base + ks * 16));
+      sb = mfma32(a, qf[ks], sb);
+    }
+    float gmx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int mm = mfma32_row(r, h);
+      if (!((approx >> mm) & 1u)) sb[r] = -INFINITY;
+      gmx = fmaxf(gmx, sb[r]);
+    }
+    gmx = fmaxf(gmx, xor32(gmx));
+    const float m_new = fmaxf(m_run, gmx * c);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+    if (!gamma_literal) g_run *= alpha;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
+    }
+    float psum = 0.f;
+    float gsum = 0.f;
+    bf16x8_t pbf[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r0 = 8 * s + 2 * i;
+        const float p0 = fast_exp2(fmaf(sb[r0], c, -m_new));
+        const float p1 = fast_exp2(fmaf(sb[r0 + 1], c, -m_new));
+        const int j0 = g * kGroup + mfma32_row(r0, h);
+        const int j1 = g * kGroup + mfma32_row(r0 + 1, h);
+        psum += p0 + p1;
+        gsum += p0 * (float)(j0 == NT - 1 ? last_len : BT) + p1 * (float)(j1 == NT - 1 ? last_len : BT);
+        w[i] = pack_bf16x2(p0, p1);
+      }
+      pbf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+    }
+    g_run += gsum;
+    psum += xor32(psum);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et) {
+        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Pvt, pv_base + et * 32 * PVT::ROW_BYTES + s * 16));
+        oacc[et] = mfma32(a, pbf[s], oacc[et]);
+      }
+    f32x16_t racc[D / 32];
+#pragma unroll
+    for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) racc[et][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et) {
+        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Pht, ph_base + et * 32 * PHT::ROW_BYTES + ks * 16));
+        racc[et] = mfma32(a, qf[ks], racc[et]);
+      }
+    const float f = psum * scale;
+#pragma unroll
+    for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[et][r] = fmaf(racc[et][r], f, oacc[et][r]);
+  }
+
+  // ---------------- Finalize ---------------------------------------------------
+  const float denom = (l_run + xor32(l_run)) + (g_run + xor32(g_run));
+  if (qrow < T) {
+    uint16_t* orow = o + slice + (int64_t)qrow * D;
+#pragma unroll
+    for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int e0 = et * 32 + 8 * rq + 4 * h;
+        uint2 w;
+        w.x = pack_bf16x2(oacc[et][4 * rq + 0] / denom, oacc[et][4 * rq + 1] / denom);
+        w.y = pack_bf16x2(oacc[et][4 * rq + 2] / denom, oacc[et][4 * rq + 3] / denom);
+        *(uint2*)(orow + e0) = w;
+      }
+  }
+}
+
+hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
+                              int bh, int T, int D, int BT, hipStream_t stream) {
+  const int NT = (T + BT - 1) / BT;
+  const int NG = (NT + kGroup - 1) / kGroup;
+  dim3 grid(NG, bh);
+  auto out = (unsigned char*)pack;
+  if (D == 128 && BT == 128)
+    hipLaunchKernelGGL((k4_pack<128, 128>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+  else if (D == 128 && BT == 64)
+    hipLaunchKernelGGL((k4_pack<128, 64>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+  else if (D == 64 && BT == 128)
+    hipLaunchKernelGGL((k4_pack<64, 128>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+  else if (D == 64 && BT == 64)
+    hipLaunchKernelGGL((k4_pack<64, 64>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
+                              const int32_t* idx, const uint32_t* selmask, void* o, float scale,
+                              int bh, int T, int D, int BT, int NS, int gamma_literal,
+                              hipStream_t stream) {
+  const int NT = (T + BT - 1) / BT;
+  const int NG = (NT + kGroup - 1) / kGroup;
+  const int NW = (NT + 31) / 32;
+  const int xcd_chunk = (NT + 7) / 8;
+  dim3 grid(8 * bh * xcd_chunk);
+  const float c = scale * kLog2e;
+  auto a = (const uint16_t*)q;
+  auto b = (const uint16_t*)k;
+  auto cc = (const uint16_t*)v;
+  auto pk = (const unsigned char*)pack;
+  auto oo = (uint16_t*)o;
+#define PASA_K4_LAUNCH(DD, BB)                                                                   \
+  hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
+                     b, cc, pk, idx, selmask, oo, scale, c, T, NT, NS, NG, NW, xcd_chunk,         \
+                     gamma_literal)
+  if (D == 128 && BT == 128)
+    PASA_K4_LAUNCH(128, 128);
+  else if (D == 128 && BT == 64)
+    PASA_K4_LAUNCH(128, 64);
+  else if (D == 64 && BT == 128)
+    PASA_K4_LAUNCH(64, 128);
+  else if (D == 64 && BT == 64)
+    PASA_K4_LAUNCH(64, 64);
+  else
+    return hipErrorInvalidValue;
+#undef PASA_K4_LAUNCH
+  return hipGetLastError();
+}
+
+}  // namespace pasa

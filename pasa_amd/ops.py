@@ -1,0 +1,214 @@
+"""PISA-PG sparse attention on MI355X: the Python operator layer.
+
+``pisa_pg_attention`` keeps the signature of the reference operator
+(svg/kernels/triton/group_pisa_attention.py:307-318) so that the attention
+processors call it unchanged.  Each stage is also exposed on its own:
+
+* ``block_stats``        K2  (reference :66-129, :268-301)
+* ``select_blocks``      K3  (reference :365-375)
+* ``select_from_scores`` K3's top-k on given scores (bit-exact parity entry)
+* ``sparse_attn``        K4  (reference :135-262)
+
+All device work goes through libpasa_amd.so (ctypes, ``pasa_amd._lib``).  This
+module allocates outputs and workspace with torch's caching allocator and passes
+torch's current HIP stream; nothing here synchronises.  There is no CPU path:
+tensors must live on a ROCm device and the library must be built.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+GROUP_SIZE = 32
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check_device(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("PISA kernels need ROCm device tensors (there is no CPU path)")
+        if not t.is_contiguous():
+            raise ValueError("PISA kernels need contiguous tensors")
+
+
+def num_selected(density: float, num_blocks: int) -> int:
+    """NS = min(max(1, int(density * NT)), NT) (reference :373), via the C ABI."""
+    ns = _lib.load().pasa_num_selected(float(density), int(num_blocks))
+    if ns < 0:
+        _lib.check("pasa_num_selected", int(ns))
+    return int(ns)
+
+
+@dataclass
+class BlockStats:
+    """Outputs of K2.  All fp32.  qc/kc/vc [B,H,NT,D], hnorm [B,H,NT], hgroup [B,H,NG,D,D]."""
+    qc: torch.Tensor
+    kc: torch.Tensor
+    vc: torch.Tensor
+    hnorm: torch.Tensor
+    hgroup: torch.Tensor
+
+
+def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int = 64,
+                group_size: int = GROUP_SIZE) -> BlockStats:
+    """Block means of Q/K, block sums of V, ||H_j||_F and the group mean of H_j.
+
+    Replaces fused_chunk_reduce (reference :268-288; hc is never materialised)
+    followed by compute_h_group (:291-301)."""
+    _check_device(q, k, v)
+    B, H, T, D = q.shape
+    NT = math.ceil(T / block_size)
+    NG = math.ceil(NT / group_size)
+    f32 = dict(device=q.device, dtype=torch.float32)
+    qc = torch.empty(B, H, NT, D, **f32)
+    kc = torch.empty(B, H, NT, D, **f32)
+    vc = torch.empty(B, H, NT, D, **f32)
+    hnorm = torch.empty(B, H, NT, **f32)
+    hgroup = torch.empty(B, H, NG, D, D, **f32)
+    _lib.call("pasa_block_stats", q.data_ptr(), k.data_ptr(), v.data_ptr(), qc.data_ptr(),
+              kc.data_ptr(), vc.data_ptr(), hnorm.data_ptr(), hgroup.data_ptr(), B * H, T, D,
+              block_size, group_size, _DTYPES.get(q.dtype, -1), _stream(q))
+    return BlockStats(qc, kc, vc, hnorm, hgroup)
+
+
+@dataclass
+class Selection:
+    """Outputs of K3.  idx int32 [B,H,NT,NS] (score desc, index asc); selmask int32 view of
+    uint32 words [B,H,NT,ceil(NT/32)]; scores fp32 [B,H,NT,NT] when requested."""
+    idx: torch.Tensor
+    selmask: torch.Tensor
+    scores: Optional[torch.Tensor]
+    ns: int
+
+
+def select_blocks(stats: BlockStats, density: float, scale: float, use_cov_bias: bool = True,
+                  noise: Optional[torch.Tensor] = None, return_scores: bool = False) -> Selection:
+    """Covariance-aware top-k of key blocks per query block (reference :365-375).
+
+    ``noise``: optional fp32 [B,H,NT], one draw per key block (the reference's
+    ``use_random``), added to the log bias only when ``use_cov_bias``."""
+    qc, kc, hnorm = stats.qc, stats.kc, stats.hnorm
+    _check_device(qc, kc, hnorm)
+    B, H, NT, D = qc.shape
+    ns = num_selected(density, NT)
+    idx = torch.empty(B, H, NT, ns, device=qc.device, dtype=torch.int32)
+    nw = (NT + 31) // 32
+    selmask = torch.empty(B, H, NT, nw, device=qc.device, dtype=torch.int32)
+    if noise is not None:
+        _check_device(noise)
+        if noise.dtype != torch.float32 or noise.numel() != B * H * NT:
+            raise ValueError("noise must be fp32 with B*H*NT elements")
+    scores = torch.empty(B, H, NT, NT, device=qc.device, dtype=torch.float32)
+    _lib.call("pasa_select", qc.data_ptr(), kc.data_ptr(), hnorm.data_ptr(), _ptr(noise),
+              float(scale), float(density), int(bool(use_cov_bias)), idx.data_ptr(),
+              selmask.data_ptr(), scores.data_ptr(), None, 0, B * H, NT, D, _stream(qc))
+    return Selection(idx, selmask, scores if return_scores else None, ns)
+
+
+def select_from_scores(scores: torch.Tensor, ns: int) -> Selection:
+    """Top-``ns`` of fp32 scores [B,H,NT,NT] with ties to the lowest index."""
+    _check_device(scores)
+    if scores.dtype != torch.float32:
+        raise ValueError("scores must be fp32")
+    B, H, NT, NT2 = scores.shape
+    if NT != NT2:
+        raise ValueError("scores must be [B,H,NT,NT]")
+    idx = torch.empty(B, H, NT, int(ns), device=scores.device, dtype=torch.int32)
+    selmask = torch.empty(B, H, NT, (NT + 31) // 32, device=scores.device, dtype=torch.int32)
+    _lib.call("pasa_select_from_scores", scores.data_ptr(), int(ns), idx.data_ptr(),
+              selmask.data_ptr(), B * H, NT, _stream(scores))
+    return Selection(idx, selmask, scores, int(ns))
+
+
+def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64) -> torch.Tensor:
+    """bf16 phase-2 operands (kbar, V^T, Hbar^T) per (slice, group), as K4 stages them in LDS."""
+    B, H, T, D = q.shape
+    lib = _lib.load()
+    nbytes = int(lib.pasa_sparse_attn_workspace_bytes(B * H, T, D, block_size, GROUP_SIZE))
+    if nbytes == 0:
+        raise ValueError(f"unsupported shape for the gfx950 kernels: D={D}, block_size={block_size}")
+    pack = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    _check_device(stats.kc, stats.vc, stats.hgroup)
+    _lib.call("pasa_pack_phase2", stats.kc.data_ptr(), stats.vc.data_ptr(), stats.hgroup.data_ptr(),
+              pack.data_ptr(), pack.numel(), B * H, T, D, block_size, GROUP_SIZE, _stream(q))
+    return pack
+
+
+def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: torch.Tensor,
+                       sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """K4 on operands from ``pack_phase2``."""
+    _check_device(q, k, v, pack)
+    if gamma not in ("literal", "consistent"):
+        raise ValueError("gamma must be 'literal' or 'consistent'")
+    B, H, T, D = q.shape
+    o = torch.empty_like(v) if out is None else out
+    _check_device(o)
+    _lib.call("pasa_sparse_attn_packed", q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(),
+              pack.numel(), sel.idx.data_ptr(), sel.selmask.data_ptr(), o.data_ptr(), float(scale),
+              B * H, T, D, block_size, GROUP_SIZE, sel.ns, int(gamma == "literal"),
+              _DTYPES.get(q.dtype, -1), _stream(q))
+    return o
+
+
+def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockStats,
+                sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Exact attention over the selected blocks plus the per-group first-order
+    correction of the rest (reference pisa_pg_fwd_kernel :135-262)."""
+    pack = pack_phase2(q, stats, block_size)
+    return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out)
+
+
+def pisa_pg_attention(
+    q, k, v,
+    density=0.15,
+    timestep=0,
+    block_size=64,
+    group_size=32,
+    scale=None,
+    use_cov_bias=True,
+    use_random=False,
+    verbose=False,
+    prompt_token_length: Optional[int] = None,
+    *,
+    noise: Optional[torch.Tensor] = None,
+    gamma: str = "literal",
+):
+    """PISA with per-group first-order correction (drop-in for reference :307-398).
+
+    q, k, v: [B, H, T, D] contiguous bf16 on a ROCm device; returns o like v.
+    ``timestep``, ``verbose`` and ``prompt_token_length`` do not change the math
+    (as in the reference, where ``prompt_token_length`` is documented but unused).
+    ``use_random`` adds one N(0,1) draw per key block to the selection score; pass
+    ``noise`` (fp32 [B,H,NT]) to make it reproducible, else it is drawn on the
+    device from torch's default generator like the reference's ``randn_like``.
+    ``gamma='consistent'`` rescales the zero-order denominator with the running max
+    (the reference's literal form does not)."""
+    B, H, T, D = q.shape
+    if group_size != GROUP_SIZE:
+        raise ValueError(f"the gfx950 kernels use group_size={GROUP_SIZE}")
+    scale = D ** -0.5 if scale is None else scale
+    NT = math.ceil(T / block_size)
+    stats = block_stats(q, k, v, block_size, group_size)
+    if use_random and use_cov_bias and noise is None:
+        noise = torch.randn(B, H, NT, device=q.device, dtype=torch.float32)
+    sel = select_blocks(stats, density, scale, use_cov_bias, noise if use_cov_bias else None)
+    if verbose:
+        print(f"NT={NT}, N_GROUPS={stats.hgroup.shape[2]}, GROUP_SIZE={group_size}")
+        print(f"top_k={sel.ns}, density={density}")
+    return sparse_attn(q, k, v, stats, sel, scale, block_size, gamma)

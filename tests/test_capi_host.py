@@ -1,0 +1,191 @@
+"""Host-side tests of the C ABI: the library loads, exports every entry point the
+header declares, and every validation error path returns its status code and
+message before any HIP call (so these run without a GPU)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from pasa_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "pasa.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pasa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built: run `python -m pasa_amd.build`")
+    return _lib.load()
+
+
+def test_exports_match_header(lib):
+    declared = header_functions()
+    assert declared, "no declarations parsed"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (pasa_[a-z0-9_]+)$", out, flags=re.M))
+    assert set(declared) <= exported, set(declared) - exported
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_version_and_status_strings(lib):
+    assert lib.pasa_abi_version() == _lib.ABI_VERSION
+    for code in _lib.STATUS:
+        assert lib.pasa_status_string(code)
+    assert lib.pasa_status_string(12345) == b"unknown status"
+
+
+@pytest.mark.parametrize("density,nt,expect", [
+    (0.1, 591, 59), (0.15, 256, 38), (0.25, 16, 4), (0.10, 929, 92), (1.0, 10, 10),
+    (0.0, 10, 1), (2.0, 10, 10), (0.29, 100, 28), (-0.5, 8, 1), (0.999999, 3, 2)])
+def test_num_selected_matches_python(lib, density, nt, expect):
+    assert lib.pasa_num_selected(density, nt) == expect == min(max(1, int(density * nt)), nt)
+
+
+def test_num_selected_errors(lib):
+    assert lib.pasa_num_selected(float("nan"), 10) == -9
+    assert b"finite" in lib.pasa_last_error()
+    assert lib.pasa_num_selected(float("inf"), 10) == -9
+    assert lib.pasa_num_selected(0.5, 0) == -2
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def permute(lib, **kw):
+    a = dict(src0=FAKE, src1=FAKE * 2, src2=FAKE * 3, dst0=FAKE * 4, dst1=FAKE * 5, dst2=FAKE * 6,
+             n=3, bh=2, F=4, P=8, ctx=0, D=128, dtype=0, mask=None, inverse=0)
+    a.update(kw)
+    return lib.pasa_permute(a["src0"], a["src1"], a["src2"], a["dst0"], a["dst1"], a["dst2"], a["n"],
+                            a["bh"], a["F"], a["P"], a["ctx"], a["D"], a["dtype"], a["mask"],
+                            a["inverse"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(n=0), -9, b"n_tensors"),
+    (dict(n=4), -9, b"n_tensors"),
+    (dict(src1=None), -1, b"NULL"),
+    (dict(dst2=None), -1, b"NULL"),
+    (dict(dtype=7), -7, b"dtype"),
+    (dict(D=100), -3, b"multiple of 16"),
+    (dict(D=4, dtype=0), -3, b"multiple of 16"),
+    (dict(F=0), -2, b"num_frame"),
+    (dict(ctx=-1), -2, b"context_length"),
+    (dict(bh=0), -2, b"must be > 0"),
+    (dict(bh=70000), -6, b"exceeds"),
+    (dict(F=1 << 20, P=1 << 20), -6, b"overflows"),
+    (dict(inverse=2), -9, b"inverse"),
+    (dict(dst0=FAKE), -9, b"overlaps"),
+])
+def test_permute_validation(lib, kw, code, msg):
+    assert permute(lib, **kw) == code
+    assert msg in lib.pasa_last_error()
+
+
+def stats(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, qc=FAKE, kc=FAKE, vc=FAKE, hn=FAKE, hg=FAKE, bh=4, T=1000,
+             D=128, BT=128, G=32, dtype=0)
+    a.update(kw)
+    return lib.pasa_block_stats(a["q"], a["k"], a["v"], a["qc"], a["kc"], a["vc"], a["hn"], a["hg"],
+                                a["bh"], a["T"], a["D"], a["BT"], a["G"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(q=None), -1), (dict(hg=None), -1), (dict(dtype=2), -7), (dict(dtype=1), -7),
+    (dict(D=96), -3), (dict(BT=32), -4), (dict(T=0), -2), (dict(bh=-1), -2), (dict(G=0), -12),
+    (dict(T=1 << 31), -6), (dict(T=(1 << 24) - 100), -6),
+])
+def test_block_stats_validation(lib, kw, code):
+    assert stats(lib, **kw) == code
+    assert lib.pasa_last_error()
+
+
+def select(lib, **kw):
+    a = dict(qc=FAKE, kc=FAKE, hn=FAKE, noise=None, scale=0.1, density=0.1, cov=1, idx=FAKE,
+             mask=FAKE, scores=FAKE, ws=None, wsb=0, bh=2, nt=100, D=128)
+    a.update(kw)
+    return lib.pasa_select(a["qc"], a["kc"], a["hn"], a["noise"], a["scale"], a["density"], a["cov"],
+                           a["idx"], a["mask"], a["scores"], a["ws"], a["wsb"], a["bh"], a["nt"],
+                           a["D"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(qc=None), -1), (dict(idx=None), -1), (dict(hn=None), -1), (dict(nt=0), -2),
+    (dict(nt=5000), -13), (dict(D=32), -3), (dict(scale=float("inf")), -9),
+    (dict(density=float("nan")), -9), (dict(scores=None), -8),
+    (dict(scores=None, ws=FAKE, wsb=100), -8), (dict(bh=1 << 20), -6),
+])
+def test_select_validation(lib, kw, code):
+    assert select(lib, **kw) == code
+    assert lib.pasa_last_error()
+
+
+def test_select_from_scores_validation(lib):
+    f = lib.pasa_select_from_scores
+    assert f(None, 1, FAKE, FAKE, 1, 10, None) == -1
+    assert f(FAKE, 0, FAKE, FAKE, 1, 10, None) == -5
+    assert f(FAKE, 11, FAKE, FAKE, 1, 10, None) == -5
+    assert f(FAKE, 3, FAKE, FAKE, 1, 4097, None) == -13
+    assert lib.pasa_select_workspace_bytes(2, 10) == 800
+    assert lib.pasa_select_workspace_bytes(0, 10) == 0
+
+
+def attn(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, kc=FAKE, vc=FAKE, hg=FAKE, idx=FAKE, mask=FAKE, o=FAKE, scale=0.1,
+             bh=2, T=1000, D=128, BT=128, G=32, ns=2, lit=1, dtype=0, ws=FAKE, wsb=1 << 30)
+    a.update(kw)
+    return lib.pasa_sparse_attn(a["q"], a["k"], a["v"], a["kc"], a["vc"], a["hg"], a["idx"], a["mask"],
+                                a["o"], a["scale"], a["bh"], a["T"], a["D"], a["BT"], a["G"], a["ns"],
+                                a["lit"], a["dtype"], a["ws"], a["wsb"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(o=None), -1), (dict(idx=None), -1), (dict(dtype=2), -7), (dict(D=256), -3),
+    (dict(BT=256), -4), (dict(G=16), -12), (dict(ns=0), -5), (dict(ns=9), -5),
+    (dict(scale=0.0), -9), (dict(scale=-1.0), -9), (dict(scale=float("nan")), -9),
+    (dict(lit=2), -9), (dict(ws=None), -8), (dict(wsb=10), -8), (dict(T=0), -2),
+    (dict(T=(1 << 24) - 100), -6),
+])
+def test_sparse_attn_validation(lib, kw, code):
+    assert attn(lib, **kw) == code
+    assert lib.pasa_last_error()
+
+
+def test_packed_entry_validation(lib):
+    pk = lib.pasa_pack_phase2
+    need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 128, 128, 32)
+    assert pk(FAKE, FAKE, FAKE, FAKE, need - 1, 2, 1000, 128, 128, 32, None) == -8
+    assert pk(None, FAKE, FAKE, FAKE, need, 2, 1000, 128, 128, 32, None) == -1
+    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 128, 128, 16, None) == -12
+    f = lib.pasa_sparse_attn_packed
+    args = [FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, 2, 1000, 128, 128, 32, 2, 1, 0, None]
+    bad = list(args); bad[4] = 0
+    assert f(*bad) == -8
+    bad = list(args); bad[14] = 100
+    assert f(*bad) == -5
+    bad = list(args); bad[16] = 2
+    assert f(*bad) == -7
+
+
+def test_workspace_bytes(lib):
+    f = lib.pasa_sparse_attn_workspace_bytes
+    # c2: 40 slices, NT = 591, NG = 19 groups of a padded 57344-byte LDS image
+    assert f(40, 75600, 128, 128, 32) == 40 * 19 * 57344
+    assert f(40, 75600, 128, 128, 16) == 0
+    assert f(1, 1024, 64, 64, 32) > 0
+
+
+def test_last_error_cleared_on_success(lib):
+    assert lib.pasa_num_selected(float("nan"), 10) < 0
+    assert lib.pasa_last_error() != b""
+    assert lib.pasa_num_selected(0.5, 10) == 5
+    assert lib.pasa_last_error() == b""

@@ -1,0 +1,243 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle (run with -m gpu).
+
+K1 (permutation) and K3's top-k are compared bit-exactly; K2 statistics and K3
+scores to fp32 tolerance; K4 and the whole op to the north_star tolerance:
+cosine >= 0.999 and max|err| <= 2e-2 * RMS(reference output), the reference
+being the oracle's fp32 evaluation of the same bf16 inputs."""
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pisa_oracle as O
+from pasa_amd import _lib, ops, placement
+from pasa_amd.workloads import WORKLOADS, Workload, make_inputs, small_workload
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.999
+MAXABS_OVER_RMS = 2e-2
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def check_parity(out, ref, what):
+    m = O.parity_metrics(out, ref)
+    say(f"[parity] {what}: cos={m['cos']:.6f} max_abs/rms={m['max_abs_over_rms']:.3e}")
+    assert m["cos"] >= COS_MIN, (what, m)
+    assert m["max_abs_over_rms"] <= MAXABS_OVER_RMS, (what, m)
+    return m
+
+
+def test_native_library_loaded(device):
+    lib = _lib.load()
+    assert lib.pasa_abi_version() == _lib.ABI_VERSION
+    maps = open("/proc/self/maps").read()
+    assert str(_lib.LIB_PATH) in maps
+
+
+# ---------------------------------------------------------------- K1 --------
+
+def random_bits(shape, device, dtype=torch.bfloat16, seed=0):
+    g = torch.Generator(device=device).manual_seed(seed)
+    if dtype == torch.float32:
+        return torch.randint(-2**31, 2**31 - 1, shape, device=device, dtype=torch.int32, generator=g).view(torch.float32)
+    return torch.randint(-2**15, 2**15 - 1, shape, device=device, dtype=torch.int16, generator=g).view(dtype)
+
+
+def as_np_bits(t):
+    return t.cpu().view(torch.int32 if t.dtype == torch.float32 else torch.int16).numpy()
+
+
+@pytest.mark.parametrize("B,H,F,P,ctx,D,dtype", [
+    (1, 12, 21, 1560, 0, 128, torch.bfloat16),      # c1: 21 frames x 30*52 patches
+    (2, 4, 11, 4080, 226, 64, torch.bfloat16),      # the reference self-test shape (placement.py:189-197), 4 heads
+    (1, 3, 33, 3600, 256, 128, torch.bfloat16),     # HunyuanVideo 720p layout with text tail, 3 heads
+    (1, 2, 5, 7, 3, 64, torch.float32),
+])
+def test_permute_bit_exact(device, B, H, F, P, ctx, D, dtype):
+    S = ctx + F * P
+    say(f"[K1] B={B} H={H} F={F} P={P} ctx={ctx} D={D} {dtype}")
+    src = [random_bits((B, H, S, D), device, dtype, seed=i) for i in range(3)]
+    dst = [torch.empty_like(t) for t in src]
+    placement.permute(src, dst, F, P, ctx, inverse=False)
+    for s, d in zip(src, dst):
+        np.testing.assert_array_equal(as_np_bits(d), O.permute(as_np_bits(s), F, P, ctx, inverse=False))
+    back = torch.empty_like(src[0])
+    placement.permute([dst[0]], [back], F, P, ctx, inverse=True)
+    assert torch.equal(back.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       src[0].view(torch.int16 if dtype != torch.float32 else torch.int32))
+    inv = torch.empty_like(src[1])
+    placement.permute([src[1]], [inv], F, P, ctx, inverse=True)
+    np.testing.assert_array_equal(as_np_bits(inv), O.permute(as_np_bits(src[1]), F, P, ctx, inverse=True))
+
+
+def test_reference_placement_api_with_head_mask(device):
+    ctx, F, P, B, H, D = 226, 11, 408, 2, 6, 64
+    S = ctx + F * P
+    say("[K1] hunyuan_sparse_head_placement / hidden_states_placement with best_mask_idx")
+    q, k, v = (random_bits((B, H, S, D), device, seed=10 + i) for i in range(3))
+    mask = torch.tensor([[1, 0, 1, 1, 0, 0], [0, 1, 1, 0, 1, 0]], device=device)
+    qo, ko, vo = (torch.empty_like(t) for t in (q, k, v))
+    placement.hunyuan_sparse_head_placement(q, k, v, qo, ko, vo, mask, ctx, F, P)
+    m = mask.cpu().numpy()
+    for s, d in ((q, qo), (k, ko), (v, vo)):
+        np.testing.assert_array_equal(as_np_bits(d), O.permute(as_np_bits(s), F, P, ctx, head_is_temporal=m))
+    ho = torch.empty_like(qo)
+    placement.hunyuan_hidden_states_placement(qo, ho, mask, ctx, F, P)
+    assert torch.equal(ho.view(torch.int16), q.view(torch.int16))
+    t = q.clone()
+    placement.hunyuan_token_reorder_to_token_major(t, ctx, F * P, F, P)
+    np.testing.assert_array_equal(as_np_bits(t), O.permute(as_np_bits(q), F, P, ctx))
+    placement.hunyuan_token_reorder_to_frame_major(t, ctx, F * P, F, P)
+    assert torch.equal(t.view(torch.int16), q.view(torch.int16))
+
+
+# ---------------------------------------------------------------- K2 --------
+
+STAT_CASES = [
+    # (heads, grid, D, BT)
+    (2, (4, 16, 16), 64, 64),        # c0 shape
+    (2, (3, 10, 20), 128, 128),      # T = 600: ragged last block (88 rows)
+    (3, (5, 13, 17), 64, 128),       # T = 1105, NT = 9
+    (1, (21, 30, 52), 128, 128),     # c1 shape, one head: NT = 256, 8 groups
+    (1, (9, 45, 80), 128, 64),       # NT = 507: 16 groups, last one partial
+]
+
+
+def bf16_inputs(heads, grid, D, BT, seed=0, density=0.15):
+    wl = Workload("t", heads=heads, head_dim=D, grid=grid, block_size=BT, density=density,
+                  prescale=D ** -0.5 / 128 ** -0.5 if D != 128 else 1.0)
+    return wl, make_inputs(wl, seed=seed, dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("heads,grid,D,BT", STAT_CASES)
+def test_block_stats(device, heads, grid, D, BT):
+    wl, (q, k, v) = bf16_inputs(heads, grid, D, BT)
+    say(f"[K2] heads={heads} T={wl.seq_len} D={D} BT={BT}")
+    st = ops.block_stats(q.to(device), k.to(device), v.to(device), BT, 32)
+    T = wl.seq_len
+    ref = O.block_stats(*(t.reshape(heads, T, D) for t in (q, k, v)), BT, dtype=torch.float64)
+    hg = O.group_moment(ref.hc, 32)
+    def close(got, exp, name, rtol=2e-5):
+        got = got.cpu().double().reshape(exp.shape)
+        tol = rtol * float(exp.abs().max()) + 1e-6
+        err = float((got - exp).abs().max())
+        say(f"[K2]   {name}: max err {err:.3e} (tol {tol:.3e})")
+        assert err <= tol, name
+    close(st.qc, ref.qc, "qc")
+    close(st.kc, ref.kc, "kc")
+    close(st.vc, ref.vc, "vc")
+    close(st.hnorm, ref.hnorm, "hnorm", 1e-4)
+    close(st.hgroup, hg, "hgroup", 1e-4)
+
+
+# ---------------------------------------------------------------- K3 --------
+
+@pytest.mark.parametrize("NT,ns", [(16, 4), (100, 15), (591, 59), (929, 92), (1024, 1), (4096, 409), (3, 3)])
+def test_select_from_scores_bit_exact(device, NT, ns):
+    say(f"[K3] select_from_scores NT={NT} ns={ns}")
+    g = torch.Generator().manual_seed(NT)
+    BH = 3
+    s = torch.randn(1, BH, NT, NT, generator=g)
+    s[0, 0] = torch.round(s[0, 0] * 2) / 2            # heavy ties
+    s[0, 1, :, ::3] = 0.0
+    s[0, 1, :, 1::3] = -0.0                           # -0.0 ties with +0.0
+    s[0, 2, 0] = 1.0                                  # an all-equal row
+    sel = ops.select_from_scores(s.to(device), ns)
+    want = O.topk_indices(s, ns)
+    np.testing.assert_array_equal(sel.idx.cpu().numpy(), want.numpy())
+    np.testing.assert_array_equal(sel.selmask.cpu().numpy().view(np.uint32), O.selection_mask(want, NT))
+
+
+@pytest.mark.parametrize("heads,grid,D,BT,density,use_noise", [
+    (2, (4, 16, 16), 64, 64, 0.25, False),
+    (2, (21, 30, 52), 128, 128, 0.15, True),
+    (1, (21, 45, 80), 128, 128, 0.10, False),
+])
+def test_select(device, heads, grid, D, BT, density, use_noise):
+    wl, (q, k, v) = bf16_inputs(heads, grid, D, BT)
+    say(f"[K3] select heads={heads} T={wl.seq_len} density={density} noise={use_noise}")
+    st = ops.block_stats(q.to(device), k.to(device), v.to(device), BT, 32)
+    NT = st.qc.shape[2]
+    noise = torch.randn(1, heads, NT, generator=torch.Generator().manual_seed(3)) if use_noise else None
+    scale = D ** -0.5
+    sel = ops.select_blocks(st, density, scale, True, None if noise is None else noise.to(device),
+                            return_scores=True)
+    ref = O.select_scores(st.qc.cpu().double(), st.kc.cpu().double(), st.hnorm.cpu().double(), scale,
+                          True, None if noise is None else noise.double())
+    got = sel.scores.cpu().double()
+    err = float((got - ref).abs().max())
+    say(f"[K3]   score max err {err:.3e}")
+    assert err <= 1e-5 * float(ref.abs().max()) + 1e-5
+    want = O.topk_indices(sel.scores.cpu(), sel.ns)
+    np.testing.assert_array_equal(sel.idx.cpu().numpy(), want.numpy())
+
+
+# ---------------------------------------------------------------- K4 --------
+
+ATTN_CASES = [
+    # heads, grid, D, BT, density, gamma
+    (2, (4, 16, 16), 64, 64, 0.25, "literal"),      # c0 shape in bf16
+    (2, (3, 10, 20), 128, 128, 0.4, "literal"),     # ragged last block
+    (2, (3, 10, 20), 128, 128, 0.4, "consistent"),
+    (2, (5, 13, 17), 64, 128, 0.3, "literal"),
+    (1, (9, 45, 80), 128, 64, 0.1, "literal"),      # BT 64, NT 507
+    (2, (21, 30, 52), 128, 128, 0.15, "literal"),   # c1 shape, 2 heads
+]
+
+
+@pytest.mark.parametrize("heads,grid,D,BT,density,gamma", ATTN_CASES)
+def test_sparse_attn_shared_selection(device, heads, grid, D, BT, density, gamma):
+    wl, (q, k, v) = bf16_inputs(heads, grid, D, BT, seed=1)
+    say(f"[K4] heads={heads} T={wl.seq_len} D={D} BT={BT} density={density} gamma={gamma}")
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    scale = D ** -0.5
+    st = ops.block_stats(qd, kd, vd, BT, 32)
+    sel = ops.select_blocks(st, density, scale)
+    o = ops.sparse_attn(qd, kd, vd, st, sel, scale, BT, gamma)
+    ref = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, gamma=gamma, indices=sel.idx.cpu())
+    check_parity(o.cpu(), ref, f"K4 {wl.seq_len}x{D} BT{BT} {gamma}")
+
+
+def test_full_density_equals_dense_attention(device):
+    wl, (q, k, v) = bf16_inputs(2, (3, 10, 20), 128, 128, seed=2)
+    say("[K4] density 1.0 vs softmax attention")
+    o = ops.pisa_pg_attention(q.to(device), k.to(device), v.to(device), density=1.0, block_size=128)
+    ref = O.dense_attention(q.double(), k.double(), v.double(), O.effective_scale(128 ** -0.5))
+    check_parity(o.cpu(), ref, "density=1")
+
+
+def test_end_to_end_c1_two_heads_with_noise(device):
+    wl = small_workload(WORKLOADS["c1"], heads=2, grid=WORKLOADS["c1"].grid)
+    q, k, v = make_inputs(wl, seed=0)
+    say(f"[E2E] c1 shape, 2 heads, T={wl.seq_len}, use_random noise")
+    NT = wl.num_blocks()
+    noise = torch.randn(1, 2, NT, generator=torch.Generator().manual_seed(5))
+    o = ops.pisa_pg_attention(q.to(device), k.to(device), v.to(device), density=wl.density,
+                              block_size=wl.block_size, scale=wl.op_scale, use_random=True,
+                              noise=noise.to(device))
+    ref = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, noise=noise)
+    check_parity(o.cpu(), ref, "c1 end-to-end")
+
+
+def test_end_to_end_c2_full_shape(device):
+    wl = WORKLOADS["c2"]
+    say(f"[E2E] c2 full shape: {wl.heads} heads x {wl.seq_len} tokens (oracle on heads 0 and 39)")
+    q, k, v = make_inputs(wl, seed=0)
+    o = ops.pisa_pg_attention(q.to(device), k.to(device), v.to(device), density=wl.density,
+                              block_size=wl.block_size, scale=wl.op_scale)
+    o2 = ops.pisa_pg_attention(q.to(device), k.to(device), v.to(device), density=wl.density,
+                               block_size=wl.block_size, scale=wl.op_scale)
+    assert torch.equal(o.view(torch.int16), o2.view(torch.int16)), "run-to-run bitwise determinism"
+    oc = o.cpu()
+    for h in (0, wl.heads - 1):
+        sl = slice(h, h + 1)
+        ref = O.pisa_pg_attention(q[:, sl], k[:, sl], v[:, sl], wl.density, wl.block_size, 32, wl.op_scale)
+        check_parity(oc[:, sl], ref, f"c2 head {h}")

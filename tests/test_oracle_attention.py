@@ -1,0 +1,171 @@
+"""Pins the oracle's PISA-PG attention (reference group_pisa_attention.py:154-262).
+
+Two independent restatements are cross-checked (the vectorised closed form and
+the literal sequential loop), and the closed form is tied to mathematics that
+fixes it: softmax attention when nothing is approximated, invariances, the
+first-order Taylor expansion for G = 1, and O(eps^2) convergence."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pisa_oracle as O
+
+f64 = torch.float64
+
+
+def rand_qkv(B, H, T, D, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn(B, H, T, D, generator=g, dtype=f64) * scale for _ in range(3))
+
+
+@pytest.mark.parametrize("T,bt,G,density,gamma", [
+    (96, 16, 2, 0.34, "literal"), (96, 16, 2, 0.34, "consistent"),
+    (100, 16, 3, 0.25, "literal"), (70, 8, 4, 0.2, "literal"), (64, 16, 32, 0.25, "literal"),
+    (45, 16, 1, 0.5, "literal")])
+def test_closed_form_matches_sequential_loop(T, bt, G, density, gamma):
+    q, k, v = rand_qkv(1, 2, T, 6, seed=T + bt + G, scale=1.5)
+    s = 6 ** -0.5
+    out, aux = O.pisa_pg_attention(q, k, v, density, bt, G, s, gamma=gamma, dtype=f64, return_aux=True)
+    for b in range(2):
+        ref = O.pisa_pg_attention_loop(q[0, b], k[0, b], v[0, b], aux["idx"][b], bt, G, s, gamma)
+        torch.testing.assert_close(out[0, b], ref, rtol=1e-10, atol=1e-10)
+
+
+def test_literal_and_consistent_differ_only_when_phase2_raises_max():
+    # A constant key block has H = 0, so its selection score carries log(1e-6) and it
+    # stays unselected, while its mean score is large: phase 2 raises the running max.
+    q, k, v = rand_qkv(1, 1, 128, 8, seed=1, scale=1.0)
+    k = k.clone()
+    k[..., 32:48, :] = 4.0 * q[0, 0, :, :].mean(0) / q[0, 0, :, :].mean(0).norm()
+    k[..., 80:96, :] = 6.0
+    lit = O.pisa_pg_attention(q, k, v, 0.125, 16, 2, 8 ** -0.5, gamma="literal", dtype=f64)
+    con = O.pisa_pg_attention(q, k, v, 0.125, 16, 2, 8 ** -0.5, gamma="consistent", dtype=f64)
+    assert not torch.allclose(lit, con)
+    # with queries/keys constant per block the selection holds the per-row maximum,
+    # phase 2 never raises it and the two forms coincide
+    qc, kc = const_blocks(q, 16), const_blocks(k, 16)
+    lit = O.pisa_pg_attention(qc, kc, v, 0.125, 16, 2, 8 ** -0.5, gamma="literal", dtype=f64)
+    con = O.pisa_pg_attention(qc, kc, v, 0.125, 16, 2, 8 ** -0.5, gamma="consistent", dtype=f64)
+    torch.testing.assert_close(lit, con, rtol=1e-12, atol=1e-12)
+
+
+def const_blocks(x, bt):
+    B, H, T, D = x.shape
+    nt = math.ceil(T / bt)
+    xb = torch.cat([x, x.new_zeros(B, H, nt * bt - T, D)], 2).reshape(B, H, nt, bt, D)
+    return xb[:, :, :, :1, :].expand(B, H, nt, bt, D).reshape(B, H, nt * bt, D)[:, :, :T].contiguous()
+
+
+@pytest.mark.parametrize("T,bt", [(128, 16), (100, 16), (64, 64)])
+def test_full_density_is_softmax_attention(T, bt):
+    q, k, v = rand_qkv(1, 2, T, 8, seed=T, scale=1.2)
+    s = 0.4
+    out = O.pisa_pg_attention(q, k, v, 1.0, bt, 4, s, dtype=f64)
+    torch.testing.assert_close(out, O.dense_attention(q, k, v, O.effective_scale(s)), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("density", [0.1, 0.25, 0.5])
+def test_constant_blocks_is_softmax_attention(density):
+    # q, k constant per block => H = 0, the selection takes each row's largest
+    # block scores, and the zero-order terms are exact.
+    q, k, v = rand_qkv(1, 2, 160, 8, seed=7, scale=1.0)
+    q, k = const_blocks(q, 16), const_blocks(k, 16)
+    s = 8 ** -0.5
+    out = O.pisa_pg_attention(q, k, v, density, 16, 4, s, dtype=f64)
+    torch.testing.assert_close(out, O.dense_attention(q, k, v, O.effective_scale(s)), rtol=1e-10, atol=1e-10)
+
+
+def test_key_shift_invariance():
+    q, k, v = rand_qkv(1, 2, 112, 8, seed=9)
+    delta = torch.randn(8, dtype=f64) * 0.7
+    a = O.pisa_pg_attention(q, k, v, 0.3, 16, 2, 0.5, dtype=f64)
+    b = O.pisa_pg_attention(q, k + delta, v, 0.3, 16, 2, 0.5, dtype=f64)
+    torch.testing.assert_close(a, b, rtol=1e-9, atol=1e-9)
+
+
+def test_value_shift_equivariance_consistent():
+    q, k, v = rand_qkv(1, 2, 112, 8, seed=10)
+    delta = torch.randn(8, dtype=f64)
+    a = O.pisa_pg_attention(q, k, v, 0.3, 16, 2, 0.5, gamma="consistent", dtype=f64)
+    b = O.pisa_pg_attention(q, k, v + delta, 0.3, 16, 2, 0.5, gamma="consistent", dtype=f64)
+    torch.testing.assert_close(b, a + delta, rtol=1e-9, atol=1e-9)
+
+
+def brute_first_order(q, k, v, idx, bt, s):
+    """G = 1: exact on selected blocks, e^{s q.kbar}(Vhat + s H^T q) on the others."""
+    T, D = q.shape
+    nt = math.ceil(T / bt)
+    se = O.effective_scale(s)   # exponent temperature; the first-order term keeps s
+    out = torch.zeros(T, D, dtype=f64)
+    for I in range(nt):
+        sel = set(idx[I].tolist())
+        for i in range(I * bt, min(T, (I + 1) * bt)):
+            num = torch.zeros(D, dtype=f64)
+            den = torch.tensor(0.0, dtype=f64)
+            for j in range(nt):
+                rows = list(range(j * bt, min(T, (j + 1) * bt)))
+                if j in sel:
+                    for t in rows:
+                        w = torch.exp(se * (q[i] @ k[t]))
+                        num += w * v[t]
+                        den += w
+                else:
+                    kb = k[rows].mean(0)
+                    vh = v[rows].sum(0)
+                    Hj = sum(torch.outer(k[t] - kb, v[t]) for t in rows)
+                    w = torch.exp(se * (q[i] @ kb))
+                    num += w * (vh + s * (Hj.T @ q[i]))
+                    den += w * len(rows)
+            out[i] = num / den
+    return out
+
+
+def test_group_size_one_is_first_order_taylor():
+    q, k, v = rand_qkv(1, 1, 72, 5, seed=12)
+    s = 0.45
+    out, aux = O.pisa_pg_attention(q, k, v, 0.2, 16, 1, s, gamma="consistent", dtype=f64, return_aux=True)
+    ref = brute_first_order(q[0, 0], k[0, 0], v[0, 0], aux["idx"][0], 16, s)
+    torch.testing.assert_close(out[0, 0], ref, rtol=1e-10, atol=1e-10)
+
+
+def test_first_order_error_is_quadratic():
+    # keys = block mean + eps * zero-mean perturbation; fixed selection; G = 1.
+    g = torch.Generator().manual_seed(13)
+    T, D, bt = 96, 6, 16
+    nt = T // bt
+    q = torch.randn(1, 1, T, D, generator=g, dtype=f64)
+    v = torch.randn(1, 1, T, D, generator=g, dtype=f64)
+    centres = torch.randn(nt, D, generator=g, dtype=f64).repeat_interleave(bt, 0)
+    pert = torch.randn(T, D, generator=g, dtype=f64).reshape(nt, bt, D)
+    pert = (pert - pert.mean(1, keepdim=True)).reshape(T, D)
+    idx = torch.tensor([[i] for i in range(nt)], dtype=torch.int32)[None, None]
+    errs = []
+    for eps in (0.2, 0.1, 0.05):
+        k = (centres + eps * pert)[None, None]
+        approx = O.pisa_pg_attention(q, k, v, block_size=bt, group_size=1, scale=0.5,
+                                     gamma="consistent", indices=idx, dtype=f64)
+        errs.append(float((approx - O.dense_attention(q, k, v, O.effective_scale(0.5))).abs().max()))
+    r1, r2 = errs[0] / errs[1], errs[1] / errs[2]
+    assert 3.0 < r1 < 5.0 and 3.3 < r2 < 4.7, errs
+
+
+def test_explicit_indices_and_noise():
+    q, k, v = rand_qkv(1, 1, 96, 8, seed=14)
+    out, aux = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, 0.5, dtype=f64, return_aux=True)
+    again = O.pisa_pg_attention(q, k, v, block_size=16, group_size=2, scale=0.5,
+                                indices=aux["idx"].reshape(1, 1, 6, -1), dtype=f64)
+    torch.testing.assert_close(out, again, rtol=0, atol=0)
+    noise = torch.randn(1, 1, 6, dtype=f64) * 50  # dominates the score
+    _, aux2 = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, 0.5, noise=noise, dtype=f64, return_aux=True)
+    top = torch.argsort(noise.reshape(-1), descending=True)[:1]
+    assert all(int(row[0]) == int(top[0]) for row in aux2["idx"][0])
+
+
+def test_parity_metrics():
+    a = torch.tensor([1.0, 2.0, 3.0])
+    m = O.parity_metrics(a, a)
+    assert m["cos"] == pytest.approx(1.0) and m["max_abs"] == 0.0
+    m = O.parity_metrics(a + torch.tensor([0.0, 0.0, 0.1]), a)
+    assert m["max_abs"] == pytest.approx(0.1, abs=1e-6)
