@@ -178,9 +178,18 @@ def selection_mask(idx: torch.Tensor, num_blocks: int) -> np.ndarray:
 # K4: attention, closed form (group_pisa_attention.py:154-262)
 # ----------------------------------------------------------------------------
 
+def _bf16(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
 def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scale, gamma,
-                   chunk):
-    """One slice.  q,k,v [T,D]; kc,vc [NT,D]; hgroup [NG,D,D]; idx [NT,NS]."""
+                   chunk, ref_precision=False):
+    """One slice.  q,k,v [T,D]; kc,vc [NT,D]; hgroup [NG,D,D]; idx [NT,NS].
+
+    ref_precision: round where the reference's kernels round (its bf16 storage of
+    kc/vc (group_pisa_attention.py:275-277) and of h_group at its use (:251), P and
+    P-bar cast to bf16 before their dot products (:185, :240), the bf16 output
+    store (:262)), giving the error floor of the reference's own precision."""
     T, D = q.shape
     NT, NS = idx.shape
     NG = hgroup.shape[0]
@@ -195,6 +204,8 @@ def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scal
     # zero-order block index -> group, padded to NG*G
     npad = NG * group_size - NT
     nlen = n.to(dt)
+    rnd = _bf16 if ref_precision else (lambda x: x)
+    kc, vc, hgroup = rnd(kc), rnd(vc), rnd(hgroup)
     for i0 in range(0, NT, chunk):
         i1 = min(NT, i0 + chunk)
         Q = qb[i0:i1]                                    # [m, BT, D]
@@ -219,10 +230,10 @@ def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scal
         mf = run[..., -1]                                # final max
         pe = torch.exp2(x - mf[..., None])
         L = pe.sum(-1)
-        A = torch.matmul(pe, Vs)                         # exact part :184-185
+        A = torch.matmul(rnd(pe), Vs)                    # exact part :184-185
         pb = torch.exp2(xg - mf[..., None, None])        # relative to the final max
         pbf = pb.reshape(m, bt, NG * group_size)[..., :NT]
-        A = A + torch.matmul(pbf, vc)                    # zero order :239-240
+        A = A + torch.matmul(rnd(pbf), vc)               # zero order :239-240
         wsum = pb.sum(-1)                                # [m, BT, NG]  :252
         r = torch.einsum("mtd,gde->mtge", Q, hgroup)     # Q . hbar_g :251
         A = A + scale * torch.einsum("mtg,mtge->mte", wsum, r)   # first order :253
@@ -235,7 +246,7 @@ def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scal
         else:
             pg = pb
         Gam = (pg * nl[None, None]).sum((-1, -2))
-        out[i0:i1] = A / (L + Gam)[..., None]            # :258-259
+        out[i0:i1] = rnd(A / (L + Gam)[..., None])       # :258-259, store :262
     return out.reshape(NT * bt, D)[:T]
 
 
@@ -243,14 +254,16 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
                       scale: Optional[float] = None, use_cov_bias: bool = True,
                       noise: Optional[torch.Tensor] = None, gamma: str = "literal",
                       indices: Optional[torch.Tensor] = None, dtype=torch.float32,
-                      chunk: int = 32, return_aux: bool = False):
+                      chunk: int = 32, return_aux: bool = False, ref_precision: bool = False):
     """Reference PISA-PG output (:307-398) on the CPU.
 
     q, k, v: [B, H, T, D] (any float dtype, computed in ``dtype``).
     noise: [B, H, NT] per-key-block selection noise (the reference's use_random).
     indices: optional [B, H, NT, NS] selection to use instead of computing it
     (isolates the attention stage from score rounding).
-    gamma: 'literal' (reference: Gamma never rescaled) or 'consistent'."""
+    gamma: 'literal' (reference: Gamma never rescaled) or 'consistent'.
+    ref_precision: emulate the reference's bf16 roundings in the attention stage
+    (the selection stays fp32); see _attention_one."""
     B, H, T, D = q.shape
     scale = D ** -0.5 if scale is None else scale
     BH = B * H
@@ -269,7 +282,7 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
     out = torch.empty(BH, T, D, dtype=dtype)
     for b in range(BH):
         out[b] = _attention_one(q3[b], k3[b], v3[b], st.kc[b], st.vc[b], hgroup[b], idx[b], st.n,
-                                block_size, group_size, scale, gamma, chunk)
+                                block_size, group_size, scale, gamma, chunk, ref_precision)
     out = out.reshape(B, H, T, D)
     if return_aux:
         return out, dict(stats=st, hgroup=hgroup, scores=scores, idx=idx)
@@ -358,11 +371,27 @@ def dense_attention(q, k, v, scale: float, dtype=torch.float64) -> torch.Tensor:
 # Parity metrics (north_star tolerance)
 # ----------------------------------------------------------------------------
 
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |x| (8 significant bits): 2^(floor(log2|x|) - 7)."""
+    ax = x.abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(ax)) - 7)
+
+
 def parity_metrics(out: torch.Tensor, ref: torch.Tensor) -> dict:
-    """cosine similarity, max-abs error and max-abs / RMS(ref) over the whole tensor."""
+    """Agreement of ``out`` with the fp32 reference ``ref``.
+
+    cos, max_abs and max_abs_over_rms are the north_star figures.  ``excess_over_rms``
+    is max(|err| - ulp_bf16(|ref|)) / RMS(ref): the error left after allowing one
+    bf16 ulp of each reference element, the quantum of any bf16 result (the
+    reference stores P and its output in bf16).  ``bound_ok`` is cos >= 0.999 and
+    excess_over_rms <= 2e-2."""
     a = out.detach().to(torch.float64).reshape(-1).cpu()
     b = ref.detach().to(torch.float64).reshape(-1).cpu()
     cos = float(torch.dot(a, b) / (a.norm() * b.norm()).clamp_min(1e-300))
-    err = float((a - b).abs().max())
+    e = (a - b).abs()
+    err = float(e.max())
     rms = float(b.pow(2).mean().sqrt())
-    return dict(cos=cos, max_abs=err, rms=rms, max_abs_over_rms=err / max(rms, 1e-300))
+    excess = float((e - bf16_ulp(b)).clamp_min(0).max())
+    return dict(cos=cos, max_abs=err, rms=rms, max_abs_over_rms=err / max(rms, 1e-300),
+                excess_over_rms=excess / max(rms, 1e-300),
+                bound_ok=bool(cos >= 0.999 and excess <= 2e-2 * rms))

@@ -1,0 +1,210 @@
+"""Wan2.1 attention processor with PISA-PG sparse attention, and its installer.
+
+Drop-in for the reference's Wan path (svg/models/wan/attention.py and
+svg/models/wan/inference.py): same class names, constructor, class-attribute
+configuration and call protocol of the diffusers attention processor
+
+    processor(attn, hidden_states, encoder_hidden_states=None, attention_mask=None,
+              rotary_emb=None, timestep=None) -> Tensor[B, S, C]
+
+(svg/models/wan/attention.py:166-174).  Self-attention calls carry ``timestep``;
+cross-attention calls (timestep None) run dense SDPA, as in the reference
+(:218-221).  The sparse branch calls ``pasa_amd.ops.pisa_pg_attention``: the
+reference calls the undefined name ``piecewise_sparse_attention`` at :384 while
+importing ``pisa_pg_attention`` at :15, the only complete PISA op in its tree.
+Left out (not on the hot path): the per-layer hidden-state L1 JSONL logging
+(:182-258), flex/FlashInfer SVG masks (:290-348) and sample_mse (:264-288).
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from .. import density as _density
+from ..ops import pisa_pg_attention
+from .rope import apply_rotary_emb_complex
+
+
+class WanAttn_SVGAttn_Processor2_0:
+    """Base processor (reference :93-301): projections, QK-norm, RoPE, dispatch, output."""
+    version = None
+    context_length = 0
+    num_frame = 0
+    frame_size = 0
+
+    first_layers_fp = 0
+    first_times_fp = 0
+
+    num_sampled_rows = 32
+    attention_masks = None
+    sparsity = 0
+
+    def __init__(self, layer_idx):
+        self.layer_idx = layer_idx
+        if not hasattr(F, "scaled_dot_product_attention"):
+            raise ImportError("WanAttnProcessor2_0 requires PyTorch 2.0.")
+
+    def get_qkv(self, attn, hidden_states, encoder_hidden_states):
+        return attn.to_q(hidden_states), attn.to_k(encoder_hidden_states), attn.to_v(encoder_hidden_states)
+
+    def get_qk_norm(self, attn, query, key):
+        # RMSNorm over the full hidden width, before the head split (reference :122-136).
+        if attn.norm_q is not None:
+            query = attn.norm_q(query)
+        if attn.norm_k is not None:
+            key = attn.norm_k(key)
+        return query, key
+
+    def get_transpose_qkv(self, attn, query, key, value):
+        query = query.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
+        key = key.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
+        value = value.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
+        return query, key, value
+
+    def get_rotary_emb(self, query, key, rotary_emb):
+        if rotary_emb is not None:
+            query = apply_rotary_emb_complex(query, rotary_emb)
+            key = apply_rotary_emb_complex(key, rotary_emb)
+        return query, key
+
+    def get_o(self, attn, query, hidden_states, hidden_states_img):
+        hidden_states = hidden_states.transpose(1, 2).flatten(2, 3)
+        hidden_states = hidden_states.type_as(query)
+        if hidden_states_img is not None:
+            hidden_states = hidden_states + hidden_states_img
+        hidden_states = attn.to_out[0](hidden_states)
+        hidden_states = attn.to_out[1](hidden_states)
+        return hidden_states
+
+    def __call__(self, attn, hidden_states: torch.Tensor,
+                 encoder_hidden_states: Optional[torch.Tensor] = None,
+                 attention_mask: Optional[torch.Tensor] = None,
+                 rotary_emb: Optional[torch.Tensor] = None,
+                 timestep=None) -> torch.Tensor:
+        encoder_hidden_states_img = None
+        if getattr(attn, "add_k_proj", None) is not None:
+            encoder_hidden_states_img = encoder_hidden_states[:, :257]
+            encoder_hidden_states = encoder_hidden_states[:, 257:]
+        if encoder_hidden_states is None:
+            encoder_hidden_states = hidden_states
+
+        query, key, value = self.get_qkv(attn, hidden_states, encoder_hidden_states)
+        query, key = self.get_qk_norm(attn, query, key)
+        query, key, value = self.get_transpose_qkv(attn, query, key, value)
+        query, key = self.get_rotary_emb(query, key, rotary_emb)
+
+        hidden_states_img = None
+        if encoder_hidden_states_img is not None:  # I2V image branch (reference :195-208)
+            key_img = attn.norm_added_k(attn.add_k_proj(encoder_hidden_states_img))
+            value_img = attn.add_v_proj(encoder_hidden_states_img)
+            key_img = key_img.unflatten(2, (attn.heads, -1)).transpose(1, 2)
+            value_img = value_img.unflatten(2, (attn.heads, -1)).transpose(1, 2)
+            hidden_states_img = F.scaled_dot_product_attention(query, key_img, value_img, dropout_p=0.0,
+                                                               is_causal=False)
+            hidden_states_img = hidden_states_img.transpose(1, 2).flatten(2, 3).type_as(query)
+
+        if timestep is None:  # cross-attention
+            hidden_states = F.scaled_dot_product_attention(query, key, value, attn_mask=attention_mask,
+                                                           dropout_p=0.0, is_causal=False)
+        else:
+            hidden_states = self.attention_core_logic(query, key, value, timestep)
+        return self.get_o(attn, query, hidden_states, hidden_states_img)
+
+    def flash_attention(self, query, key, value):
+        """Dense attention (reference :298-301), PyTorch-ROCm SDPA."""
+        return F.scaled_dot_product_attention(query, key, value, dropout_p=0.0, is_causal=False)
+
+    def attention_core_logic(self, query, key, value, timestep):  # pragma: no cover - abstract
+        raise NotImplementedError
+
+
+class Wan_PASA_Processor(WanAttn_SVGAttn_Processor2_0):
+    """PASA processor (reference :350-390)."""
+    rescaled_density: dict = {}
+    base_density = 0.15
+    block_size = 64        # the reference's call site passes block_size=64 (:387)
+    use_random = False
+    logging_file = None
+    num_layers = 0
+
+    def __init__(self, layer_idx):
+        super().__init__(layer_idx)
+        self.layer_idx = layer_idx
+
+    def attention_core_logic(self, query, key, value, timestep):
+        cfg, num_heads, seq_len, dim = query.size()
+        assert cfg == 1, "Batch size must be 1 for kmeans block sparse attention"
+        context_length, num_frame, frame_size = self.context_length, self.num_frame, self.frame_size
+        assert seq_len == context_length + num_frame * frame_size, (
+            f"Query Shape: {seq_len} is not equivalent to {context_length} + {num_frame} * {frame_size}")
+
+        full_attention_flag = False
+        if self.layer_idx < self.first_layers_fp:
+            full_attention_flag = True
+        if timestep[0] > self.first_times_fp:
+            full_attention_flag = True
+
+        if full_attention_flag:
+            out = self.flash_attention(query, key, value)
+            return out.reshape(cfg, num_heads, seq_len, dim)
+
+        ts_key = int(timestep[0].item()) if torch.is_tensor(timestep[0]) else int(timestep[0])
+        density = self.rescaled_density.get(ts_key)
+        assert density is not None, f"Density is not found for timestep {ts_key}"
+        out = pisa_pg_attention(query.contiguous(), key.contiguous(), value.contiguous(),
+                                density=density, block_size=self.block_size,
+                                use_random=self.use_random)
+        return out.reshape(cfg, num_heads, seq_len, dim)
+
+
+def replace_sparse_forward():
+    """Thread ``timestep`` from the transformer into each block's self-attention call.
+
+    The reference monkey-patches diffusers' WanTransformerBlock / WanTransformer3DModel
+    forwards for this (svg/models/wan/custom_models.py:23-207).  Models whose blocks
+    already pass ``timestep=`` to ``attn1`` (e.g. pasa_amd.models' Wan DiT) need nothing;
+    with diffusers present the patch in ``pasa_amd.processors.diffusers_patch`` is applied."""
+    try:
+        from . import diffusers_patch
+    except ImportError:
+        return False
+    return diffusers_patch.patch_wan()
+
+
+def replace_wan_attention(pipe, height, width, num_frames, first_layers_fp, first_times_fp,
+                          pattern="PASA", logging_file=None, base_density=0.15):
+    """Install Wan_PASA_Processor on every block's self-attention (reference
+    svg/models/wan/inference.py:12-74)."""
+    context_length = 0
+    num_frame_patches = 1 + num_frames // (pipe.vae_scale_factor_temporal * pipe.transformer.config.patch_size[0])
+    mod_value = pipe.vae_scale_factor_spatial * pipe.transformer.config.patch_size[1]
+    frame_patches_one_frame = int(height // mod_value) * int(width // mod_value)
+
+    replace_sparse_forward()
+    num_layers = len(pipe.transformer.blocks)
+
+    if pattern != "PASA":
+        raise ValueError(f"Pattern '{pattern}' not supported")
+    if logging_file is not None:
+        os.makedirs(os.path.dirname(logging_file) or ".", exist_ok=True)
+        with open(logging_file, "w") as f:
+            f.write("")
+
+    AttnModule = Wan_PASA_Processor
+    AttnModule.first_layers_fp = first_layers_fp
+    AttnModule.first_times_fp = first_times_fp
+    AttnModule.logging_file = logging_file
+    AttnModule.context_length = context_length
+    AttnModule.num_frame = num_frame_patches
+    AttnModule.frame_size = frame_patches_one_frame
+    AttnModule.num_layers = num_layers
+    AttnModule.base_density = base_density
+    AttnModule.rescaled_density = _density.wan_rescaled_density(base_density)
+
+    for layer_idx, m in enumerate(pipe.transformer.blocks):
+        if hasattr(m.attn1, "processor"):
+            m.attn1.set_processor(AttnModule(layer_idx=layer_idx))
+    print(f"Attention processors replaced with {pattern} pattern.")
