@@ -125,10 +125,13 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
                             int64_t bh, int64_t num_blocks, void* stream);
 
 /* ---- K4: block-sparse attention with per-group first-order correction -----
- * For query block I: exact online-softmax attention over the key blocks idx[I]
- * (in the order given), then for each group g of 32 key blocks the zero-order
- * (kc, vc) plus first-order (hgroup) contribution of the blocks of g not in
- * idx[I], merged into the same running max; o = A / (L + Gamma).
+ * For query block I: exact online-softmax attention over the key blocks selected
+ * in selmask[I], then for each group g of 32 key blocks the zero-order (kc, vc)
+ * plus first-order (hgroup) contribution of the blocks of g not selected, merged
+ * into the same running max; o = A / (L + Gamma).  The kernel reads the selection
+ * from selmask only (idx must be the matching index list, as pasa_select writes
+ * it, but is not read): the exact blocks are visited in ascending block order,
+ * which equals the reference's top-k order up to floating-point rounding.
  * gamma_literal = 1 reproduces the reference exactly: Gamma (the zero-order
  * denominator, sum p_j * n_j) is not rescaled when the running max rises;
  * gamma_literal = 0 rescales it with A and L.

@@ -128,6 +128,34 @@ __device__ __forceinline__ float xor32(float x) {
   return __shfl_xor(x, 32, 64);
 }
 
+// max / sum of x over lanes l and l ^ 32, identical on both lanes
+// (v_permlane32_swap exchanges the two wave halves in the VALU).
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum of the two bf16 halves of w, accumulated into acc (v_dot2c_f32_bf16 with ones).
+__device__ __forceinline__ float bf16x2_sum(uint32_t w, float acc) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, the 64-bit loads of lanes
+// 4r..4r+3 form row r (16 consecutive 16-bit elements) of a 4 x 16 block, and
+// lane i of the group receives column i: {row0[i], row1[i], row2[i], row3[i]}.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const unsigned char* base, int byte_off) {
+  typedef __attribute__((address_space(3))) s16x4_t* lds_v4_ptr;
+  const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4_ptr)(base + byte_off));
+  return __builtin_bit_cast(uint2, r);
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);

@@ -2,7 +2,7 @@
 //
 // Reference: pisa_pg_fwd_kernel, svg/kernels/triton/group_pisa_attention.py:135-262
 //   Phase 1 (:170-186): exact online softmax (base 2) over the selected key
-//     blocks, in top-k order; columns >= T masked.
+//     blocks; columns >= T masked.
 //   Phase 2 (:212-253): per group g of 32 key blocks, the blocks not selected
 //     contribute p_j (V^_j + s * Hbar_g^T q) with p_j = 2^(c q.kbar_j - m);
 //     A and L are rescaled when the running max rises, Gamma = sum p_j n_j is
@@ -14,16 +14,23 @@
 // wavefront per 32 query rows.  Everything is computed transposed so that a lane
 // owns one query (lane % 32) and the softmax statistics are per-lane scalars:
 //   S^T[key][q]  = K  * Q^T   (v_mfma_f32_32x32x16_bf16, K from LDS, Q in VGPRs)
-//   O^T[e][q]   += V^T * P^T   (V^T from LDS, P from the S^T accumulators)
-// The S^T accumulator of a lane already holds, per 16-key step s, exactly the 8
-// keys (16s + 8i' + 4h + j) that the lane's P^T B-operand slots need; V^T is
-// written to LDS with tokens permuted by tok_perm so the matching A-operand
-// slots are one 16-byte LDS read.  Keys of a block are consumed in halves of
-// 64 (one online-softmax step each) to bound live accumulators.
+//   O^T[e][q]   += V^T * P^T   (V^T read from the row-major V tile with
+//                               ds_read_b64_tr_b16, P from the S^T accumulators)
+// The S^T accumulator of a lane holds, per 16-key step s, exactly the 8 keys
+// (16s + 8i' + 4h + j) its P^T B-operand slots need; two transposing LDS reads
+// fetch the matching V^T slots.  Keys of a block are consumed in halves of 64
+// (one online-softmax step each) to bound live accumulators.
+//
+// Phase 1 walks the selected blocks in ascending block order (the selection
+// bitmask) instead of top-k order: exact online softmax is order-independent up
+// to rounding, and the ascending sweep keeps the workgroups of one XCD on
+// nearby key blocks at the same time, so the K/V tiles they share hit in L2.
+// The running max used for exponentiation is updated lazily (only when a row's
+// max grows by more than 2^8), and caught up to the exact phase-1 max before
+// phase 2, so phase 2 sees the same running max sequence as the reference.
 // The K/V tiles of block i+1 are fetched into registers while block i computes.
 // Workgroups are mapped XCD-aware: each XCD walks a contiguous run of query
-// blocks of the same head, so neighbouring query blocks (whose selections
-// overlap) share that XCD's L2.
+// blocks of the same head.
 //
 // Phase-2 operands (kbar, V^ transposed, Hbar transposed; bf16) are packed per
 // (slice, group) by k4_pack into the exact LDS image K4 copies in.
@@ -40,22 +47,24 @@ struct K4Cfg {
   static constexpr int THREADS = WAVES * 64;
   static constexpr int CH = D / 8;
   using KT = PadTile<D>;       // K tile:        BT rows x D
-  using VT = PadTile<BT>;      // V^T tile:      D rows x BT tokens (tok_perm order)
+  // V tile: BT rows x D, natural chunk order, row stride 2D + 64 bytes, which
+  // makes the transposing reads of 32 lanes (4 rows x 2 chunks per 16-lane
+  // group, two groups side by side) hit 64 distinct banks.
+  static constexpr int VROW = 2 * D + 64;
   using PKB = PadTile<D>;      // kbar:          32 rows x D
   using PVT = PadTile<kGroup>; // V^ transposed: D rows x 32 means (tok_perm order)
   using PHT = PadTile<D>;      // Hbar^T:        D rows (e) x D (d)
   static constexpr int KS_BYTES = KT::bytes(BT);
-  static constexpr int P1_BYTES = KS_BYTES + VT::bytes(D);
+  static constexpr int P1_BYTES = KS_BYTES + BT * VROW;
   static constexpr int PK_VT_OFF = PKB::bytes(kGroup);
   static constexpr int PK_HT_OFF = PK_VT_OFF + PVT::bytes(D);
   static constexpr int PK_RAW = PK_HT_OFF + PHT::bytes(D);
   static constexpr int PK_BYTES = (PK_RAW + 16 * THREADS - 1) / (16 * THREADS) * (16 * THREADS);
   static constexpr int LDS_BYTES = P1_BYTES > PK_BYTES ? P1_BYTES : PK_BYTES;
   static constexpr int K_LOADS = (BT * D / 8) / THREADS;   // 16-byte K chunks per thread
-  static constexpr int V_UNITS = (BT * D / 16) / THREADS;  // (2 rows x 16 bytes) V units per thread
+  static constexpr int V_LOADS = K_LOADS;                  // 16-byte V chunks per thread
   static constexpr int PK_LOADS = PK_BYTES / 16 / THREADS;
   static_assert(K_LOADS * THREADS * 8 == BT * D, "K tile split");
-  static_assert(V_UNITS * THREADS * 16 == BT * D, "V tile split");
   static_assert(THREADS % CH == 0, "K rows per pass");
 };
 
@@ -105,19 +114,19 @@ __global__ __launch_bounds__(256) void k4_pack(const float* __restrict__ kc,
 
 // ---- main kernel ------------------------------------------------------------
 
+constexpr float kRescaleThreshold = 0.0f;  // log2 units; 0 = rescale whenever a row max rises
+
 template <int D, int BT>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
 void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                     const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
-                    const int32_t* __restrict__ idx, const uint32_t* __restrict__ selmask,
-                    uint16_t* __restrict__ o, float scale, float c, int T, int NT, int NS,
-                    int NG, int NW, int xcd_chunk, int gamma_literal) {
+                    const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o, float scale,
+                    float c, int T, int NT, int NG, int NW, int xcd_chunk, int gamma_literal) {
   using C = K4Cfg<D, BT>;
   using KT = typename C::KT;
-  using VT = typename C::VT;
   __shared__ __attribute__((aligned(16))) unsigned char lds[C::LDS_BYTES];
   unsigned char* Ks = lds;
-  unsigned char* Vt = lds + C::KS_BYTES;
+  unsigned char* Vs = lds + C::KS_BYTES;
 
   // XCD-aware workgroup -> (slice, query block) map: consecutive workgroup ids
   // go to consecutive XCDs, so slot = wg / 8 indexes within one XCD's run.
@@ -152,62 +161,68 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
   for (int et = 0; et < D / 32; ++et)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[et][r] = 0.f;
-  float m_run = -INFINITY;
   float l_run = 0.f;
   float g_run = 0.f;
 
-  const int32_t* irow = idx + ((int64_t)bh * NT + qb) * NS;
+  const uint32_t* mrow = selmask + ((int64_t)bh * NT + qb) * NW;
 
-  // Lane-constant parts of the tile load / store addresses.
-  constexpr int KROWS = C::THREADS / C::CH;  // K rows covered per load pass
-  const uint32_t k_goff = (uint32_t)((tid / C::CH) * D + (tid % C::CH) * 8) * 2u;
+  // Lane-constant parts of the tile load / store / read addresses.
+  constexpr int KROWS = C::THREADS / C::CH;  // rows covered per load pass
+  const uint32_t goff = (uint32_t)((tid / C::CH) * D + (tid % C::CH) * 8) * 2u;
   const int k_soff = KT::chunk_byte(tid / C::CH, tid % C::CH);
-  const int vp = 16 * wave + (lane & 15);  // key pair (2vp, 2vp+1) this lane moves
-  const uint32_t v_goff = (uint32_t)(2 * vp * D + (lane >> 4) * 8) * 2u;
-  const int v_soff = VT::elem_byte(8 * (lane >> 4), tok_perm(2 * vp));
+  const int v_soff = (tid / C::CH) * C::VROW + (tid % C::CH) * 16;
   const int ka_base = KT::frag_base(l32, h);
-  const int va_base = VT::frag_base(l32, h);
+  // Transposing V reads: group g = lane / 16 covers keys +4*(g/2) and columns
+  // +16*(g%2); lane i of the group addresses row i/4, columns 4*(i%4) .. +3.
+  const int g16 = lane >> 4;
+  const int i16 = lane & 15;
+  const int vtr_base = (4 * (g16 >> 1) + (i16 >> 2)) * C::VROW + (16 * (g16 & 1) + 4 * (i16 & 3)) * 2;
 
   // ---------------- Phase 1: exact attention over the selected blocks --------
   uint4 kreg[C::K_LOADS];
-  uint4 vreg[C::V_UNITS][2];
+  uint4 vreg[C::V_LOADS];
   auto fetch = [&](int blk) {
-    const uint32_t base = (uint32_t)blk * BT * D * 2u;
+    const uint32_t base = (uint32_t)blk * BT * D * 2u + goff;
 #pragma unroll
-    for (int it = 0; it < C::K_LOADS; ++it)
-      kreg[it] = buf_load16(kr, base + k_goff + it * KROWS * D * 2);
+    for (int it = 0; it < C::K_LOADS; ++it) kreg[it] = buf_load16(kr, base + it * KROWS * D * 2);
 #pragma unroll
-    for (int it = 0; it < C::V_UNITS; ++it)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) vreg[it][s] = buf_load16(vr, base + v_goff + it * 64 + s * D * 2);
+    for (int it = 0; it < C::V_LOADS; ++it) vreg[it] = buf_load16(vr, base + it * KROWS * D * 2);
   };
   auto stash = [&]() {
 #pragma unroll
     for (int it = 0; it < C::K_LOADS; ++it) lds_st(Ks, k_soff + it * KROWS * KT::ROW_BYTES, kreg[it]);
 #pragma unroll
-    for (int it = 0; it < C::V_UNITS; ++it) {
-      const uint32_t a[4] = {vreg[it][0].x, vreg[it][0].y, vreg[it][0].z, vreg[it][0].w};
-      const uint32_t b[4] = {vreg[it][1].x, vreg[it][1].y, vreg[it][1].z, vreg[it][1].w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t lo = (i & 1) ? (a[i >> 1] >> 16) : (a[i >> 1] & 0xffffu);
-        const uint32_t hi = (i & 1) ? (b[i >> 1] & 0xffff0000u) : (b[i >> 1] << 16);
-        lds_st(Vt, v_soff + (32 * it + i) * VT::ROW_BYTES, lo | hi);
-      }
-    }
+    for (int it = 0; it < C::V_LOADS; ++it) lds_st(Vs, v_soff + it * KROWS * C::VROW, vreg[it]);
   };
 
-  fetch(irow[0]);
-  for (int it = 0; it < NS; ++it) {
-    const int blk = irow[it];
+  // Selected blocks in ascending order, from the selection bitmask (uniform).
+  int wsel = 0;
+  uint32_t bits = NW > 0 ? mrow[0] : 0u;
+  auto next_selected = [&]() -> int {
+    while (bits == 0u) {
+      if (++wsel >= NW) return -1;
+      bits = mrow[wsel];
+    }
+    const int j = 32 * wsel + __builtin_ctz(bits);
+    bits &= bits - 1u;
+    return j;
+  };
+
+  float m_use = -INFINITY;   // max used for exponentiation (lags m_true by < 2^8)
+  float m_true = -INFINITY;  // exact running max of the selected scores (log2 units)
+  int blk = next_selected();
+  if (blk >= 0) fetch(blk);
+  while (blk >= 0) {
+    const int nxt = next_selected();
     __syncthreads();
     stash();
     __syncthreads();
-    if (it + 1 < NS) fetch(irow[it + 1]);
+    if (nxt >= 0) fetch(nxt);
 
     const int nvalid = min(BT, T - blk * BT);
 #pragma unroll
     for (int kh = 0; kh < BT / 64; ++kh) {
+      if (kh * 64 >= nvalid) break;  // fully masked half (ragged last block)
       f32x16_t sacc[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -221,7 +236,7 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
               lds_ld<uint4>(Ks, ka_base + (kh * 64 + mt * 32) * KT::ROW_BYTES + ks * 16));
           sacc[mt] = mfma32(a, qf[ks], sacc[mt]);
         }
-      if (nvalid < BT) {
+      if (nvalid < (kh + 1) * 64) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -233,40 +248,56 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[mt][r]);
-      mx = fmaxf(mx, xor32(mx));
-      // A fully masked half (only in a ragged last block) leaves the state unchanged.
-      const float m_new = fmaxf(m_run, mx * c);
-      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-      float psum = 0.f;
+      const float mxc = halves_max(mx) * c;
+      m_true = fmaxf(m_true, mxc);
+      if (__any(mxc > m_use + kRescaleThreshold)) {
+        const float m_new = fmaxf(m_use, mxc);
+        const float alpha = fast_exp2(m_use - m_new);  // 0 on the first step
+        m_use = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
+      }
       bf16x8_t pf[4];
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         uint32_t w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p0 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i], c, -m_new));
-          const float p1 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i + 1], c, -m_new));
-          psum += p0 + p1;
+          const float p0 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i], c, -m_use));
+          const float p1 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i + 1], c, -m_use));
           w[i] = pack_bf16x2(p0, p1);
+          l_run = bf16x2_sum(w[i], l_run);
         }
         pf[s4] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
       }
-      m_run = m_new;
-      l_run = l_run * alpha + psum;
-      if (__any(alpha != 1.f)) {
 #pragma unroll
-        for (int et = 0; et < D / 32; ++et)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
-      }
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int rowk = 16 * (kh * 4 + s4);
 #pragma unroll
         for (int et = 0; et < D / 32; ++et) {
-          const bf16x8_t a = as_bf16x8(
-              lds_ld<uint4>(Vt, va_base + et * 32 * VT::ROW_BYTES + (kh * 4 + s4) * 16));
+          const int off = vtr_base + rowk * C::VROW + et * 64;
+          const uint2 lo = lds_read_tr16(Vs, off);
+          const uint2 hi = lds_read_tr16(Vs, off + 8 * C::VROW);
+          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
           oacc[et] = mfma32(a, pf[s4], oacc[et]);
         }
+      }
+    }
+    blk = nxt;
+  }
+  // Catch the lagging max up to the exact phase-1 max before phase 2.
+  float m_run = m_true;
+  if (m_true != -INFINITY) {
+    const float alpha = fast_exp2(m_use - m_true);
+    l_run *= alpha;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
     }
   }
 
@@ -281,7 +312,6 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
   const int pv_base = PVT::frag_base(l32, h);
   const int ph_base = PHT::frag_base(l32, h);
   const int last_len = T - (NT - 1) * BT;
-  const uint32_t* mrow = selmask + ((int64_t)bh * NT + qb) * NW;
   for (int g = 0; g < NG; ++g) {
     // Blocks of this group that take the approximation (uniform over the workgroup).
     const int nin = min(kGroup, NT - g * kGroup);
@@ -315,8 +345,7 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
       if (!((approx >> mm) & 1u)) sb[r] = -INFINITY;
       gmx = fmaxf(gmx, sb[r]);
     }
-    gmx = fmaxf(gmx, xor32(gmx));
-    const float m_new = fmaxf(m_run, gmx * c);
+    const float m_new = fmaxf(m_run, halves_max(gmx) * c);
     const float alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
     l_run *= alpha;
@@ -347,7 +376,7 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
       pbf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
     }
     g_run += gsum;
-    psum += xor32(psum);
+    psum = halves_sum(psum);
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -375,7 +404,7 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
   }
 
   // ---------------- Finalize ---------------------------------------------------
-  const float denom = (l_run + xor32(l_run)) + (g_run + xor32(g_run));
+  const float denom = halves_sum(l_run) + halves_sum(g_run);
   if (qrow < T) {
     uint16_t* orow = o + slice + (int64_t)qrow * D;
 #pragma unroll
@@ -427,8 +456,7 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
   auto oo = (uint16_t*)o;
 #define PASA_K4_LAUNCH(DD, BB)                                                                   \
   hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
-                     b, cc, pk, idx, selmask, oo, scale, c, T, NT, NS, NG, NW, xcd_chunk,         \
-                     gamma_literal)
+                     b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
   if (D == 128 && BT == 128)
     PASA_K4_LAUNCH(128, 128);
   else if (D == 128 && BT == 64)
