@@ -67,6 +67,41 @@ __device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t byte_off) {
   return uint4{v[0], v[1], v[2], v[3]};
 }
 
+// Bounds-checked direct load into LDS (buffer_load_dwordx4 ... lds): lane l's
+// 16 bytes at byte_off land at lds_base + 16*l (lds_base wave-uniform); lanes
+// whose range lies outside the resource write zeros.
+__device__ __forceinline__ void buf_load16_lds(rsrc_t r, unsigned char* lds_base, uint32_t byte_off,
+                                               uint32_t soff) {
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_base, 16, byte_off, soff, 0, 0);
+}
+
+// The same load issued as inline assembly, for schedules that manage vmcnt
+// themselves: the compiler then does not track these loads, so it neither
+// drains them before unrelated LDS reads nor counts them in its own waits
+// (which remain correct, as extra loads in flight only make them conservative).
+// rsrc: buffer descriptor words; lds_addr: LDS byte address (wave-uniform).
+__device__ __forceinline__ void dma_load16_lds(u32x4_t rsrc, uint32_t lds_addr, uint32_t byte_off,
+                                               uint32_t soff) {
+  // m0 is set here on every use; kernels calling this issue no compiler-generated
+  // LDS-direct loads, so nothing else relies on m0 across it.
+  // lds_addr and soff must be wave-uniform; readfirstlane puts them in SGPRs.
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(byte_off), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory");
+}
+
+__device__ __forceinline__ u32x4_t make_rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return (u32x4_t){(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // ---- LDS tile layouts -----------------------------------------------------
 
 // Padded tile of bf16 rows with COLS columns.  Row stride is COLS*2 + 16 bytes,

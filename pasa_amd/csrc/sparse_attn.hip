@@ -68,13 +68,6 @@ struct K4Cfg {
   static_assert(THREADS % CH == 0, "K rows per pass");
 };
 
-size_t k4_pack_bytes(int D, int BT) {
-  if (D == 128 && BT == 128) return K4Cfg<128, 128>::PK_BYTES;
-  if (D == 128 && BT == 64) return K4Cfg<128, 64>::PK_BYTES;
-  if (D == 64 && BT == 128) return K4Cfg<64, 128>::PK_BYTES;
-  if (D == 64 && BT == 64) return K4Cfg<64, 64>::PK_BYTES;
-  return 0;
-}
 
 // ---- phase-2 operand pack ---------------------------------------------------
 
@@ -109,6 +102,63 @@ __global__ __launch_bounds__(256) void k4_pack(const float* __restrict__ kc,
     const int d = u / D;  // Hbar[d][e] row-major in, Hbar^T[e][d] out
     const int e = u - d * D;
     *(uint16_t*)(out + C::PK_HT_OFF + C::PHT::elem_byte(e, d)) = (uint16_t)f32_to_bf16_bits(hb[u]);
+  }
+}
+
+// Phase-2 pack image for the D = 128 direct-load kernel, split between its two
+// LDS tile buffers: [Hbar^T: 128 rows x 256 B, XOR layout of a K tile] -> K buffer;
+// [kbar: 32 rows x 256 B, XOR layout][V^ transposed: PadTile<32>] -> V buffer.
+template <int BT>
+struct K4DPack {
+  static constexpr int WAVES = BT / 32;
+  static constexpr int HT_BYTES = 128 * 256;
+  static constexpr int KB_OFF = 0;                       // within the V-buffer part
+  static constexpr int VT_OFF = 32 * 256;
+  static constexpr int RAW2 = VT_OFF + PadTile<kGroup>::bytes(128);
+  static constexpr int PART2 = (RAW2 + 1024 * WAVES - 1) / (1024 * WAVES) * (1024 * WAVES);
+  static constexpr int BYTES = HT_BYTES + PART2;
+  static_assert(HT_BYTES % (1024 * WAVES) == 0, "pack split");
+};
+
+// Byte offset of element (row, col) in a 256-byte-row tile whose 16-byte chunk c
+// of row r is stored at c ^ (r & 15).
+__host__ __device__ __forceinline__ constexpr int xor_tile_byte(int row, int col) {
+  return row * 256 + ((((col >> 3) ^ row) & 15) << 4) + (col & 7) * 2;
+}
+
+template <int BT>
+__global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
+                                                   const float* __restrict__ vc,
+                                                   const float* __restrict__ hgroup,
+                                                   unsigned char* __restrict__ pack, int NT, int NG) {
+  using P = K4DPack<BT>;
+  constexpr int D = 128;
+  const int g = blockIdx.x;
+  const int bh = blockIdx.y;
+  unsigned char* out = pack + ((int64_t)bh * NG + g) * P::BYTES;
+  const float* kb = kc + (int64_t)bh * NT * D;
+  const float* vb = vc + (int64_t)bh * NT * D;
+  const float* hb = hgroup + ((int64_t)bh * NG + g) * D * D;
+  for (int u = threadIdx.x; u < D * D; u += 256) {
+    const int d = u / D;  // Hbar[d][e] row-major in, Hbar^T[e][d] out
+    const int e = u - d * D;
+    *(uint16_t*)(out + xor_tile_byte(e, d)) = (uint16_t)f32_to_bf16_bits(hb[u]);
+  }
+  unsigned char* part2 = out + P::HT_BYTES;
+  for (int u = threadIdx.x; u < kGroup * D; u += 256) {
+    const int m = u / D;
+    const int d = u - m * D;
+    const int jj = g * kGroup + m;
+    const float x = jj < NT ? kb[(int64_t)jj * D + d] : 0.f;
+    *(uint16_t*)(part2 + P::KB_OFF + xor_tile_byte(m, d)) = (uint16_t)f32_to_bf16_bits(x);
+  }
+  for (int u = threadIdx.x; u < D * kGroup; u += 256) {
+    const int m = u % kGroup;
+    const int e = u / kGroup;
+    const int jj = g * kGroup + m;
+    const float x = jj < NT ? vb[(int64_t)jj * D + e] : 0.f;
+    *(uint16_t*)(part2 + P::VT_OFF + PadTile<kGroup>::elem_byte(e, tok_perm(m))) =
+        (uint16_t)f32_to_bf16_bits(x);
   }
 }
 
@@ -420,6 +470,364 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
   }
 }
 
+// ---- D = 128: tiles loaded straight into LDS ----------------------------------
+//
+// Same computation as k4_sparse_attn, restructured for D = 128 so that the K/V
+// tiles never pass through VGPRs: buffer_load_dwordx4 ... lds writes each lane's
+// 16 bytes to LDS directly (zeros past the end of the slice), which frees the
+// staging registers for deeper LDS-operand prefetching while two workgroups
+// still share each CU.  Per block i, with one K and one V buffer:
+//   wait K_i -> barrier -> S = K_i Q^T -> wait V_i -> barrier -> load K_{i+1}
+//   -> softmax -> O += V_i P -> barrier -> load V_{i+1}
+// so K_{i+1} streams in during softmax + P.V and V_{i+1} during the next S.
+// Tiles use 256-byte rows with XOR-swizzled 16-byte chunks: K chunk c of row r
+// sits at c ^ (r & 15) (conflict-free MFMA A-operand reads of 16 rows), V chunk
+// c at c ^ 4*(r & 3) (conflict-free transposing reads).  The phase-2 pack image
+// is loaded the same way.
+
+template <int BT>
+struct K4D {
+  static constexpr int D = 128;
+  static constexpr int WAVES = BT / 32;
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int TILE = BT * 256;                   // bytes of one K or V tile
+  static constexpr int VW = 4 / WAVES;                    // 4-row load slots per wave per 16 rows
+  static constexpr int TILE_LOADS = TILE / 1024 / WAVES;  // 1 KB direct loads per wave per tile
+  using PK = K4DPack<BT>;
+  static constexpr int KBUF = TILE > PK::HT_BYTES ? TILE : PK::HT_BYTES;
+  static constexpr int VBUF = TILE > PK::PART2 ? TILE : PK::PART2;
+  static_assert(TILE_LOADS == 8, "load schedule");
+};
+
+// vmcnt-only wait (expcnt / lgkmcnt left unconstrained), gfx9 s_waitcnt encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without a memory fence, so in-flight direct-to-LDS tile loads
+// are not drained (a fenced __syncthreads would wait for them).  It is used only
+// where this wave's preceding LDS reads have been consumed by MFMAs, i.e. have
+// completed, and where the next LDS writes are direct loads issued after it.
+__device__ __forceinline__ void barrier_lds_reads_done() { __builtin_amdgcn_s_barrier(); }
+
+template <int BT>
+__global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
+void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                        const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
+                        const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o,
+                        float scale, float c, int T, int NT, int NG, int NW, int xcd_chunk,
+                        int gamma_literal) {
+  using C = K4D<BT>;
+  using PK = typename C::PK;
+  constexpr int D = 128;
+  // Two distinct LDS objects, so the compiler can tell loads into one from reads of the other.
+  __shared__ __attribute__((aligned(1024))) unsigned char Ks[C::KBUF];
+  __shared__ __attribute__((aligned(1024))) unsigned char Vs[C::VBUF];
+
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7;
+  const int slot = wg >> 3;
+  const int bh = slot / xcd_chunk;
+  const int qb = xcd * xcd_chunk + (slot - bh * xcd_chunk);
+  if (qb >= NT) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+  const int64_t slice = (int64_t)bh * T * D;
+  const int qrow = qb * BT + wave * 32 + l32;
+
+  const uint32_t slice_bytes = (uint32_t)T * D * 2u;
+  const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
+
+  bf16x8_t qf[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    qf[ks] = as_bf16x8(buf_load16(qr, ((uint32_t)qrow * D + ks * 16 + h * 8) * 2u));
+  // Complete the Q loads now: vector-memory waits the compiler would place at their
+  // first use inside the loop would also wait for the tile loads in flight there.
+  wait_vmcnt<0>();
+
+  f32x16_t oacc[D / 32];
+#pragma unroll
+  for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[et][r] = 0.f;
+  float l_run = 0.f;
+  float g_run = 0.f;
+  float m_run = -INFINITY;
+
+  // The selection row is read-only here: constant address space -> scalar loads,
+  // which wait on lgkmcnt and leave the in-flight tile loads alone.
+  typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+  const const_u32_ptr mrow = (const_u32_ptr)(selmask + ((int64_t)bh * NT + qb) * NW);
+
+  // Direct-load lane constants.  Load (vw, n) of this wave covers tile rows
+  // 16n + 4*(wave + WAVES*vw) + lane/16; the lane's 16 bytes land at chunk lane % 16.
+  const int lrow = lane >> 4;
+  const int lch = lane & 15;
+  uint32_t k_lane[C::VW];
+#pragma unroll
+  for (int vw = 0; vw < C::VW; ++vw) {
+    const int r = 4 * (wave + C::WAVES * vw) + lrow;  // row mod 16
+    k_lane[vw] = (uint32_t)(r * 256 + ((lch ^ r) << 4));
+  }
+  const uint32_t v_lane0 = (uint32_t)((4 * wave + lrow) * 256 + ((lch ^ (4 * lrow)) << 4));
+
+  const u32x4_t kd = make_rsrc_words(k + slice, slice_bytes);
+  const u32x4_t vd = make_rsrc_words(v + slice, slice_bytes);
+  const uint32_t ks_lds = lds_addr(Ks);
+  const uint32_t vs_lds = lds_addr(Vs);
+  auto load_k = [&](int blk) {
+    const uint32_t soff = (uint32_t)blk * BT * 256u;
+#pragma unroll
+    for (int vw = 0; vw < C::VW; ++vw)
+#pragma unroll
+      for (int n = 0; n < BT / 16; ++n)
+        dma_load16_lds(kd, ks_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256, k_lane[vw] + 16 * n * 256, soff);
+  };
+  auto load_v = [&](int blk) {
+    const uint32_t soff = (uint32_t)blk * BT * 256u;
+#pragma unroll
+    for (int vw = 0; vw < C::VW; ++vw)
+#pragma unroll
+      for (int n = 0; n < BT / 16; ++n)
+        dma_load16_lds(vd, vs_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256,
+                       v_lane0 + (4 * C::WAVES * vw + 16 * n) * 256, soff);
+  };
+
+  // MFMA operand addresses: K-layout A fragments (also used for Hbar^T and kbar)
+  // and the transposing V reads.
+  int kofs[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) kofs[ks] = l32 * 256 + (((2 * ks + h) ^ (l32 & 15)) << 4);
+  const int g16 = lane >> 4;
+  const int i16 = lane & 15;
+  int vofs[D / 32];
+#pragma unroll
+  for (int et = 0; et < D / 32; ++et)
+    vofs[et] = (4 * (g16 >> 1) + (i16 >> 2)) * 256 +
+               ((4 * (et ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
+
+  int wsel = 0;
+  uint32_t bits = NW > 0 ? mrow[0] : 0u;
+  auto next_selected = [&]() -> int {
+    while (bits == 0u) {
+      if (++wsel >= NW) return -1;
+      bits = mrow[wsel];
+    }
+    const int j = 32 * wsel + __builtin_ctz(bits);
+    bits &= bits - 1u;
+    return j;
+  };
+
+  // ---------------- Phase 1 ------------------------------------------------------
+  int blk = next_selected();
+  if (blk >= 0) {
+    load_k(blk);
+    load_v(blk);
+  }
+  while (blk >= 0) {
+    const int nxt = next_selected();
+    wait_vmcnt<C::TILE_LOADS>();  // this wave's K_blk loads landed (V_blk may be in flight)
+    barrier_lds_reads_done();     // ... and every wave's
+
+    f32x16_t sacc[BT / 32];
+#pragma unroll
+    for (int mt = 0; mt < BT / 32; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[mt][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int mt = 0; mt < BT / 32; ++mt) {
+        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + mt * 32 * 256));
+        sacc[mt] = mfma32(a, qf[ks], sacc[mt]);
+      }
+
+    wait_vmcnt<0>();           // V_blk landed
+    barrier_lds_reads_done();  // every wave: V_blk landed, K_blk reads done
+    if (nxt >= 0) load_k(nxt);
+
+    const int nvalid = min(BT, T - blk * BT);
+    if (nvalid < BT) {
+#pragma unroll
+      for (int mt = 0; mt < BT / 32; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (mt * 32 + mfma32_row(r, h) >= nvalid) sacc[mt][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < BT / 32; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[mt][r]);
+    const float mxc = halves_max(mx) * c;
+    if (__any(mxc > m_run)) {
+      const float m_new = fmaxf(m_run, mxc);
+      const float alpha = fast_exp2(m_run - m_new);  // 0 on the first block
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
+    }
+    bf16x8_t pf[BT / 16];
+#pragma unroll
+    for (int s = 0; s < BT / 16; ++s) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p0 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i], c, -m_run));
+        const float p1 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i + 1], c, -m_run));
+        w[i] = pack_bf16x2(p0, p1);
+        l_run = bf16x2_sum(w[i], l_run);
+      }
+      pf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+    }
+#pragma unroll
+    for (int s = 0; s < BT / 16; ++s)
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et) {
+        const uint2 lo = lds_read_tr16(Vs, vofs[et] + s * 16 * 256);
+        const uint2 hi = lds_read_tr16(Vs, vofs[et] + s * 16 * 256 + 8 * 256);
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
+        oacc[et] = mfma32(a, pf[s], oacc[et]);
+      }
+    barrier_lds_reads_done();  // every wave is done reading V_blk
+    if (nxt >= 0) load_v(nxt);
+    blk = nxt;
+  }
+
+  // ---------------- Phase 2 ------------------------------------------------------
+  const int last_len = T - (NT - 1) * BT;
+  const u32x4_t pd = make_rsrc_words(pack + (int64_t)bh * NG * PK::BYTES, (uint32_t)(NG * PK::BYTES));
+  const unsigned char* Pvt = Vs + PK::VT_OFF;
+  const int pv_base = PadTile<kGroup>::frag_base(l32, h);
+  for (int g = 0; g < NG; ++g) {
+    const int nin = min(kGroup, NT - g * kGroup);
+    const uint32_t inrange = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+    const uint32_t approx = inrange & ~mrow[g];
+    if (approx == 0u) continue;
+
+    barrier_lds_reads_done();  // previous readers of both buffers are done
+    const uint32_t gsoff = (uint32_t)(g * PK::BYTES);
+#pragma unroll
+    for (int n = 0; n < PK::HT_BYTES / 1024 / C::WAVES; ++n) {
+      const int kb = n * C::WAVES + wave;  // 1 KB piece of Hbar^T
+      dma_load16_lds(pd, ks_lds + kb * 1024, (uint32_t)(kb * 1024 + lane * 16), gsoff);
+    }
+#pragma unroll
+    for (int n = 0; n < PK::PART2 / 1024 / C::WAVES; ++n) {
+      const int kb = n * C::WAVES + wave;
+      dma_load16_lds(pd, vs_lds + kb * 1024, (uint32_t)(PK::HT_BYTES + kb * 1024 + lane * 16), gsoff);
+    }
+    wait_vmcnt<0>();
+    barrier_lds_reads_done();
+
+    f32x16_t sb;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sb[r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Vs, PK::KB_OFF + kofs[ks]));
+      sb = mfma32(a, qf[ks], sb);
+    }
+    float gmx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int mm = mfma32_row(r, h);
+      if (!((approx >> mm) & 1u)) sb[r] = -INFINITY;
+      gmx = fmaxf(gmx, sb[r]);
+    }
+    const float m_new = fmaxf(m_run, halves_max(gmx) * c);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+    if (!gamma_literal) g_run *= alpha;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
+    }
+    float psum = 0.f;
+    float gsum = 0.f;
+    bf16x8_t pbf[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r0 = 8 * s + 2 * i;
+        const float p0 = fast_exp2(fmaf(sb[r0], c, -m_new));
+        const float p1 = fast_exp2(fmaf(sb[r0 + 1], c, -m_new));
+        const int j0 = g * kGroup + mfma32_row(r0, h);
+        const int j1 = g * kGroup + mfma32_row(r0 + 1, h);
+        psum += p0 + p1;
+        gsum += p0 * (float)(j0 == NT - 1 ? last_len : BT) + p1 * (float)(j1 == NT - 1 ? last_len : BT);
+        w[i] = pack_bf16x2(p0, p1);
+      }
+      pbf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+    }
+    g_run += gsum;
+    psum = halves_sum(psum);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et) {
+        const bf16x8_t a =
+            as_bf16x8(lds_ld<uint4>(Pvt, pv_base + et * 32 * PadTile<kGroup>::ROW_BYTES + s * 16));
+        oacc[et] = mfma32(a, pbf[s], oacc[et]);
+      }
+    f32x16_t racc[D / 32];
+#pragma unroll
+    for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) racc[et][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et) {
+        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
+        racc[et] = mfma32(a, qf[ks], racc[et]);
+      }
+    const float f = psum * scale;
+#pragma unroll
+    for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[et][r] = fmaf(racc[et][r], f, oacc[et][r]);
+  }
+
+  const float denom = halves_sum(l_run) + halves_sum(g_run);
+  if (qrow < T) {
+    uint16_t* orow = o + slice + (int64_t)qrow * D;
+#pragma unroll
+    for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int e0 = et * 32 + 8 * rq + 4 * h;
+        uint2 w;
+        w.x = pack_bf16x2(oacc[et][4 * rq + 0] / denom, oacc[et][4 * rq + 1] / denom);
+        w.y = pack_bf16x2(oacc[et][4 * rq + 2] / denom, oacc[et][4 * rq + 3] / denom);
+        *(uint2*)(orow + e0) = w;
+      }
+  }
+}
+
+size_t k4_pack_bytes(int D, int BT) {
+  if (D == 128 && BT == 128) return K4DPack<128>::BYTES;
+  if (D == 128 && BT == 64) return K4DPack<64>::BYTES;
+  if (D == 64 && BT == 128) return K4Cfg<64, 128>::PK_BYTES;
+  if (D == 64 && BT == 64) return K4Cfg<64, 64>::PK_BYTES;
+  return 0;
+}
+
 hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
                               int bh, int T, int D, int BT, hipStream_t stream) {
   const int NT = (T + BT - 1) / BT;
@@ -427,9 +835,9 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
   dim3 grid(NG, bh);
   auto out = (unsigned char*)pack;
   if (D == 128 && BT == 128)
-    hipLaunchKernelGGL((k4_pack<128, 128>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+    hipLaunchKernelGGL((k4_pack_xor<128>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
   else if (D == 128 && BT == 64)
-    hipLaunchKernelGGL((k4_pack<128, 64>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+    hipLaunchKernelGGL((k4_pack_xor<64>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
   else if (D == 64 && BT == 128)
     hipLaunchKernelGGL((k4_pack<64, 128>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
   else if (D == 64 && BT == 64)
@@ -458,9 +866,11 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
   hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
                      b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
   if (D == 128 && BT == 128)
-    PASA_K4_LAUNCH(128, 128);
+    hipLaunchKernelGGL((k4_sparse_attn_dma<128>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b, cc,
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal);
   else if (D == 128 && BT == 64)
-    PASA_K4_LAUNCH(128, 64);
+    hipLaunchKernelGGL((k4_sparse_attn_dma<64>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b, cc,
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal);
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
   else if (D == 64 && BT == 64)

@@ -178,8 +178,8 @@ def test_packed_entry_validation(lib):
 
 def test_workspace_bytes(lib):
     f = lib.pasa_sparse_attn_workspace_bytes
-    # c2: 40 slices, NT = 591, NG = 19 groups of a padded 57344-byte LDS image
-    assert f(40, 75600, 128, 128, 32) == 40 * 19 * 57344
+    # c2: 40 slices, NT = 591, NG = 19 groups of a 53248-byte phase-2 LDS image
+    assert f(40, 75600, 128, 128, 32) == 40 * 19 * 53248
     assert f(40, 75600, 128, 128, 16) == 0
     assert f(1, 1024, 64, 64, 32) > 0
 
