@@ -1,0 +1,343 @@
+"""HunyuanVideo attention processors with PISA-PG sparse attention, and their installers.
+
+Drop-in for the reference's HunyuanVideo path (svg/models/hyvideo/attention.py and
+svg/models/hyvideo/inference.py): same class names, constructor, class-attribute
+configuration and call protocol
+
+    processor(attn, hidden_states, encoder_hidden_states=None, attention_mask=None,
+              image_rotary_emb=None, timestep=None) -> (hidden_states, encoder_hidden_states)
+
+(svg/models/hyvideo/attention.py:341-380).  The joint sequence is
+[video tokens (frame-major), text tokens]; ``attention_mask`` ([B, 1, 1, N] bool,
+built by the model, svg/models/hyvideo/custom_models.py:174-186) marks the valid
+prefix.  Dense attention is block-diagonal over [0, valid) and [valid, N), the
+reference's varlen call with cu_seqlens = [0, mask.sum(), N] (:315-323, :450-476);
+here it is two PyTorch-ROCm SDPA calls on the two segments.
+
+Notes on the reference:
+* ``Hunyuan_PASA_Processor`` derives from ``Hunyuan_SAPAttn_Processor2_0`` (:644),
+  a name the module never defines; the evident base is ``Hunyuan_SVGAttn_Processor2_0``
+  (:234), which this module uses.
+* With ``use_group=False`` the reference calls ``piecewise_sparse_attention``
+  (svg/kernels/triton/pisa_attention.py), a different operator that is outside this
+  build; that setting raises ``NotImplementedError``.
+* The sparse call passes the whole joint sequence, text tokens included, to
+  ``pisa_pg_attention`` with block_size=64 (:680): text tokens are ordinary tokens.
+Left out (not on the hot path): sample_mse / flex-attention SVG masks (:382-411).
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from .. import density as _density
+from ..ops import pisa_pg_attention
+from ..placement import hunyuan_hidden_states_placement, hunyuan_sparse_head_placement
+from .rope import apply_rotary_emb_cos_sin
+from .timestep_hook import current_timestep, install_hunyuan
+
+
+def _split_heads(attn, x):
+    return x.unflatten(2, (attn.heads, -1)).transpose(1, 2)
+
+
+def block_diagonal_attention(query, key, value, valid: int):
+    """softmax attention restricted to [0, valid) x [0, valid) and [valid, N) x [valid, N)."""
+    N = query.shape[2]
+    if valid >= N:
+        return F.scaled_dot_product_attention(query, key, value, dropout_p=0.0, is_causal=False)
+    out = torch.empty_like(query)
+    for a, b in ((0, valid), (valid, N)):
+        if b > a:
+            out[:, :, a:b] = F.scaled_dot_product_attention(query[:, :, a:b], key[:, :, a:b], value[:, :, a:b],
+                                                            dropout_p=0.0, is_causal=False)
+    return out
+
+
+def _valid_length(attention_mask, n: int) -> int:
+    if attention_mask is None:
+        return n
+    return int(attention_mask.sum().item())
+
+
+def _rope_single(query, key, image_rotary_emb, txt_len):
+    """RoPE on the video part of a single-stream sequence (text last) (:211-223)."""
+    img_q, txt_q = query[:, :, :-txt_len], query[:, :, -txt_len:]
+    img_k, txt_k = key[:, :, :-txt_len], key[:, :, -txt_len:]
+    img_q = apply_rotary_emb_cos_sin(img_q, image_rotary_emb)
+    img_k = apply_rotary_emb_cos_sin(img_k, image_rotary_emb)
+    return torch.cat([img_q, txt_q], dim=2), torch.cat([img_k, txt_k], dim=2)
+
+
+class HunyuanVideoAttnProcessor2_0_FlashAttention:
+    """Dense processor (reference :41-157): the model's masked attention as block-diagonal
+    varlen attention."""
+
+    def __init__(self, layer_idx):
+        self.layer_idx = layer_idx
+        if not hasattr(F, "scaled_dot_product_attention"):
+            raise ImportError("HunyuanVideoAttnProcessor2_0_FlashAttention requires PyTorch 2.0.")
+
+    def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None,
+                 image_rotary_emb=None):
+        if attn.add_q_proj is None and encoder_hidden_states is not None:
+            hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
+        query = _split_heads(attn, attn.to_q(hidden_states))
+        key = _split_heads(attn, attn.to_k(hidden_states))
+        value = _split_heads(attn, attn.to_v(hidden_states))
+        if attn.norm_q is not None:
+            query = attn.norm_q(query)
+        if attn.norm_k is not None:
+            key = attn.norm_k(key)
+        if image_rotary_emb is not None:
+            if attn.add_q_proj is None and encoder_hidden_states is not None:
+                query, key = _rope_single(query, key, image_rotary_emb, encoder_hidden_states.shape[1])
+            else:
+                query = apply_rotary_emb_cos_sin(query, image_rotary_emb)
+                key = apply_rotary_emb_cos_sin(key, image_rotary_emb)
+        if attn.add_q_proj is not None and encoder_hidden_states is not None:
+            eq = _split_heads(attn, attn.add_q_proj(encoder_hidden_states))
+            ek = _split_heads(attn, attn.add_k_proj(encoder_hidden_states))
+            ev = _split_heads(attn, attn.add_v_proj(encoder_hidden_states))
+            if attn.norm_added_q is not None:
+                eq = attn.norm_added_q(eq)
+            if attn.norm_added_k is not None:
+                ek = attn.norm_added_k(ek)
+            query = torch.cat([query, eq], dim=2)
+            key = torch.cat([key, ek], dim=2)
+            value = torch.cat([value, ev], dim=2)
+        out = block_diagonal_attention(query, key, value, _valid_length(attention_mask, query.shape[2]))
+        out = out.transpose(1, 2).flatten(2, 3).to(query.dtype)
+        if encoder_hidden_states is not None:
+            out, encoder_hidden_states = out[:, : -encoder_hidden_states.shape[1]], \
+                out[:, -encoder_hidden_states.shape[1]:]
+            if getattr(attn, "to_out", None) is not None:
+                out = attn.to_out[0](out)
+                out = attn.to_out[1](out)
+            if getattr(attn, "to_add_out", None) is not None:
+                encoder_hidden_states = attn.to_add_out(encoder_hidden_states)
+        return out, encoder_hidden_states
+
+
+class Hunyuan_SVGAttn_Processor2_0:
+    """Base processor (reference :234-531): projections, QK-norm, RoPE, text concat,
+    dispatch, output projection."""
+    num_sampled_rows = 32
+    attention_masks = None
+
+    prompt_length = 0
+    context_length = 256
+    num_frame = 33
+    frame_size = 3600
+
+    first_layers_fp = 0
+    first_times_fp = 0
+
+    def __init__(self, layer_idx):
+        self.layer_idx = layer_idx
+        if not hasattr(F, "scaled_dot_product_attention"):
+            raise ImportError("Hunyuan_SparseAttn requires PyTorch 2.0, please upgrade PyTorch.")
+
+    def get_qkv(self, attn, hidden_states):
+        return attn.to_q(hidden_states), attn.to_k(hidden_states), attn.to_v(hidden_states)
+
+    def get_transpose_qkv(self, attn, query, key, value):
+        return (_split_heads(attn, query).contiguous(), _split_heads(attn, key).contiguous(),
+                _split_heads(attn, value).contiguous())
+
+    def get_qk_norm(self, attn, query, key):
+        # Per-head RMSNorm over D, after the head split (reference :275-278, :204-209).
+        if attn.norm_q is not None:
+            query = attn.norm_q(query)
+        if attn.norm_k is not None:
+            key = attn.norm_k(key)
+        return query, key
+
+    def get_rotary_emb(self, attn, query, key, image_rotary_emb, encoder_hidden_states):
+        if image_rotary_emb is not None:
+            if attn.add_q_proj is None and encoder_hidden_states is not None:
+                query, key = _rope_single(query, key, image_rotary_emb, encoder_hidden_states.shape[1])
+            else:
+                query = apply_rotary_emb_cos_sin(query, image_rotary_emb)
+                key = apply_rotary_emb_cos_sin(key, image_rotary_emb)
+        return query, key
+
+    def get_encoder_condition_and_concat(self, attn, query, key, value, encoder_hidden_states):
+        if attn.add_q_proj is not None and encoder_hidden_states is not None:
+            eq = _split_heads(attn, attn.add_q_proj(encoder_hidden_states))
+            ek = _split_heads(attn, attn.add_k_proj(encoder_hidden_states))
+            ev = _split_heads(attn, attn.add_v_proj(encoder_hidden_states))
+            if attn.norm_added_q is not None:
+                eq = attn.norm_added_q(eq)
+            if attn.norm_added_k is not None:
+                ek = attn.norm_added_k(ek)
+            query = torch.cat([query, eq], dim=2)
+            key = torch.cat([key, ek], dim=2)
+            value = torch.cat([value, ev], dim=2)
+        return query, key, value
+
+    def get_cu_max_seqlen(self, attention_mask, device):
+        """(cu_seqlens_q, cu_seqlens_kv, max_seqlen_q, max_seqlen_kv) of the two segments (:315-323)."""
+        n = attention_mask.numel()
+        cu = torch.tensor([0, int(attention_mask.sum().item()), n], dtype=torch.int32, device=device)
+        return cu, cu.clone(), n, n
+
+    def get_o(self, attn, hidden_states, encoder_hidden_states):
+        if encoder_hidden_states is not None:
+            hidden_states, encoder_hidden_states = (hidden_states[:, : -encoder_hidden_states.shape[1]],
+                                                    hidden_states[:, -encoder_hidden_states.shape[1]:])
+            if getattr(attn, "to_out", None) is not None:
+                hidden_states = attn.to_out[0](hidden_states)
+                hidden_states = attn.to_out[1](hidden_states)
+            if getattr(attn, "to_add_out", None) is not None:
+                encoder_hidden_states = attn.to_add_out(encoder_hidden_states)
+        return hidden_states, encoder_hidden_states
+
+    def __call__(self, attn, hidden_states: torch.Tensor,
+                 encoder_hidden_states: Optional[torch.Tensor] = None,
+                 attention_mask: Optional[torch.Tensor] = None,
+                 image_rotary_emb=None, timestep=None):
+        if attn.add_q_proj is None and encoder_hidden_states is not None:
+            hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
+        query, key, value = self.get_qkv(attn, hidden_states)
+        query, key, value = self.get_transpose_qkv(attn, query, key, value)
+        query, key = self.get_qk_norm(attn, query, key)
+        query, key = self.get_rotary_emb(attn, query, key, image_rotary_emb, encoder_hidden_states)
+        query, key, value = self.get_encoder_condition_and_concat(attn, query, key, value, encoder_hidden_states)
+        if attention_mask is None:
+            attention_mask = torch.ones(query.shape[2], dtype=torch.bool, device=query.device)
+        if timestep is None:
+            timestep = current_timestep()      # set by the installed forward hook
+        cu_max_seqlens = self.get_cu_max_seqlen(attention_mask, query.device)
+        hidden_states = self.attention_core_logic(query, key, value, timestep, self.layer_idx, cu_max_seqlens)
+        hidden_states = hidden_states.transpose(1, 2).flatten(2, 3).to(query.dtype)
+        return self.get_o(attn, hidden_states, encoder_hidden_states)
+
+    def flash_attention(self, query, key, value, cu_max_seqlens):
+        """Dense block-diagonal attention over the two cu_seqlens segments (:459-476)."""
+        cu = cu_max_seqlens[0]
+        return block_diagonal_attention(query, key, value, int(cu[1].item()))
+
+    def flashinfer_attention(self, query, key, value, cu_max_seqlens):
+        """Same semantics as ``flash_attention`` (the reference's FlashInfer variant, :450-457)."""
+        return self.flash_attention(query, key, value, cu_max_seqlens)
+
+    def sparse_head_placement(self, query, key, value, query_out, key_out, value_out, best_mask_idx,
+                              context_length, num_frame, frame_size):
+        hunyuan_sparse_head_placement(query, key, value, query_out, key_out, value_out, best_mask_idx,
+                                      context_length, num_frame, frame_size)
+        return query_out, key_out, value_out
+
+    fast_sparse_head_placement = sparse_head_placement
+
+    def hidden_states_placement(self, hidden_states, output_hidden_states, best_mask_idx, context_length,
+                                num_frame, frame_size):
+        hunyuan_hidden_states_placement(hidden_states, output_hidden_states, best_mask_idx, context_length,
+                                        num_frame, frame_size)
+
+    fast_hidden_states_placement = hidden_states_placement
+
+    def attention_core_logic(self, query, key, value, timestep, layer_idx, cu_max_seqlens):
+        """Dense by default; subclasses override the sparse branch."""
+        cfg, num_heads, seq_len, dim = query.size()
+        return self.flash_attention(query, key, value, cu_max_seqlens).reshape(cfg, num_heads, seq_len, dim)
+
+
+class Hunyuan_PASA_Processor(Hunyuan_SVGAttn_Processor2_0):
+    """PASA processor (reference :644-683)."""
+    rescaled_density: dict = {}
+    base_density = 0.15
+    use_group = True
+    use_random = True
+    block_size = 64        # the reference's call site passes block_size=64 (:680)
+    logging_file = None
+
+    def __init__(self, layer_idx):
+        super().__init__(layer_idx)
+
+    def attention_core_logic(self, query, key, value, timestep, layer_idx, cu_max_seqlens):
+        cfg, num_heads, seq_len, dim = query.size()
+        assert cfg == 1, "Batch size must be 1 for kmeans block sparse attention"
+        context_length, num_frame, frame_size = self.context_length, self.num_frame, self.frame_size
+        assert seq_len == context_length + num_frame * frame_size, (
+            f"Query Shape: {seq_len} is not equivalent to {context_length} + {num_frame} * {frame_size}")
+
+        full_attention_flag = False
+        if self.layer_idx < self.first_layers_fp:
+            full_attention_flag = True
+        if timestep is None or timestep[0] > self.first_times_fp:
+            full_attention_flag = True
+
+        if full_attention_flag:
+            out = self.flashinfer_attention(query, key, value, cu_max_seqlens)
+            return out.reshape(cfg, num_heads, seq_len, dim)
+
+        ts = int(timestep[0].item()) if torch.is_tensor(timestep[0]) else int(timestep[0])
+        density = _density.lookup_rescaled_density(self.rescaled_density, ts)
+        assert density is not None, f"Density is not found for timestep {ts}"
+        if not self.use_group:
+            raise NotImplementedError("use_group=False selects piecewise_sparse_attention "
+                                      "(svg/kernels/triton/pisa_attention.py), which this build does not provide")
+        out = pisa_pg_attention(query.contiguous(), key.contiguous(), value.contiguous(), density=density,
+                                block_size=self.block_size, use_random=self.use_random)
+        return out.reshape(cfg, num_heads, seq_len, dim)
+
+
+def replace_sparse_forward() -> bool:
+    """Make the denoising timestep reach every block's attention processor.
+
+    The reference replaces diffusers' HunyuanVideo block and model forwards for this
+    (svg/models/hyvideo/custom_models.py:16-263); here the model's forward is wrapped
+    (``timestep_hook``).  False when diffusers is not importable."""
+    return install_hunyuan()
+
+
+def replace_hyvideo_flashattention(pipe):
+    """Install the dense processor on every double- and single-stream block (reference
+    svg/models/hyvideo/inference.py:14-28)."""
+    n_double = len(pipe.transformer.transformer_blocks)
+    for layer_idx, m in enumerate(pipe.transformer.transformer_blocks):
+        m.attn.processor = HunyuanVideoAttnProcessor2_0_FlashAttention(layer_idx=layer_idx)
+    for layer_idx, m in enumerate(pipe.transformer.single_transformer_blocks):
+        m.attn.processor = HunyuanVideoAttnProcessor2_0_FlashAttention(layer_idx=layer_idx + n_double)
+
+
+def replace_hyvideo_attention(pipe, height, width, num_frames, prompt_length, first_layers_fp, first_times_fp,
+                              pattern="PASA", logging_file=None, base_density=0.15, use_dynamic=True,
+                              use_group=True, use_random=True) -> float:
+    """Configure and install Hunyuan_PASA_Processor (reference svg/models/hyvideo/inference.py:31-92).
+
+    The latent grid follows the reference: 256 context (text) tokens, 1 + num_frames // 4
+    latent frames of height * width / 256 tokens.  Returns width / frame_size as the
+    reference does."""
+    context_length, num_frame = 256, 1 + num_frames // 4
+    frame_size = height * width // 256
+    if pattern == "PASA":
+        if logging_file is not None:
+            os.makedirs(os.path.dirname(logging_file) or ".", exist_ok=True)
+            with open(logging_file, "w") as f:
+                f.write("")
+        M = Hunyuan_PASA_Processor
+        M.prompt_length = prompt_length
+        M.context_length = context_length
+        M.num_frame = num_frame
+        M.frame_size = frame_size
+        M.first_layers_fp = first_layers_fp
+        M.first_times_fp = first_times_fp
+        M.logging_file = logging_file
+        M.base_density = base_density
+        M.use_group = use_group
+        M.use_random = use_random
+        M.rescaled_density = _density.hunyuan_rescaled_density(base_density, use_dynamic)
+        replace_sparse_forward()
+        n_double = len(pipe.transformer.transformer_blocks)
+        for layer_idx, m in enumerate(pipe.transformer.transformer_blocks):
+            m.attn.processor = M(layer_idx=layer_idx)
+        for layer_idx, m in enumerate(pipe.transformer.single_transformer_blocks):
+            m.attn.processor = M(layer_idx=layer_idx + n_double)
+    elif pattern != "dense":
+        raise ValueError(f"Invalid pattern: {pattern}")
+    return width / frame_size

@@ -7,9 +7,9 @@ configuration and call protocol of the diffusers attention processor
     processor(attn, hidden_states, encoder_hidden_states=None, attention_mask=None,
               rotary_emb=None, timestep=None) -> Tensor[B, S, C]
 
-(svg/models/wan/attention.py:166-174).  Self-attention calls carry ``timestep``;
-cross-attention calls (timestep None) run dense SDPA, as in the reference
-(:218-221).  The sparse branch calls ``pasa_amd.ops.pisa_pg_attention``: the
+(svg/models/wan/attention.py:166-174).  Self-attention calls carry ``timestep``
+(passed in, or taken from the forward hook of ``timestep_hook``); cross-attention
+calls (timestep None) run dense SDPA, as in the reference (:218-221).  The sparse branch calls ``pasa_amd.ops.pisa_pg_attention``: the
 reference calls the undefined name ``piecewise_sparse_attention`` at :384 while
 importing ``pisa_pg_attention`` at :15, the only complete PISA op in its tree.
 Left out (not on the hot path): the per-layer hidden-state L1 JSONL logging
@@ -26,6 +26,7 @@ import torch.nn.functional as F
 from .. import density as _density
 from ..ops import pisa_pg_attention
 from .rope import apply_rotary_emb_complex
+from .timestep_hook import current_timestep, install_wan
 
 
 class WanAttn_SVGAttn_Processor2_0:
@@ -85,6 +86,7 @@ class WanAttn_SVGAttn_Processor2_0:
                  rotary_emb: Optional[torch.Tensor] = None,
                  timestep=None) -> torch.Tensor:
         encoder_hidden_states_img = None
+        self_attention = encoder_hidden_states is None
         if getattr(attn, "add_k_proj", None) is not None:
             encoder_hidden_states_img = encoder_hidden_states[:, :257]
             encoder_hidden_states = encoder_hidden_states[:, 257:]
@@ -106,6 +108,8 @@ class WanAttn_SVGAttn_Processor2_0:
                                                                is_causal=False)
             hidden_states_img = hidden_states_img.transpose(1, 2).flatten(2, 3).type_as(query)
 
+        if timestep is None and self_attention:
+            timestep = current_timestep()      # set by the installed forward hook
         if timestep is None:  # cross-attention
             hidden_states = F.scaled_dot_product_attention(query, key, value, attn_mask=attention_mask,
                                                            dropout_p=0.0, is_causal=False)
@@ -161,17 +165,13 @@ class Wan_PASA_Processor(WanAttn_SVGAttn_Processor2_0):
 
 
 def replace_sparse_forward():
-    """Thread ``timestep`` from the transformer into each block's self-attention call.
+    """Make the denoising timestep reach each block's self-attention processor.
 
-    The reference monkey-patches diffusers' WanTransformerBlock / WanTransformer3DModel
-    forwards for this (svg/models/wan/custom_models.py:23-207).  Models whose blocks
-    already pass ``timestep=`` to ``attn1`` (e.g. pasa_amd.models' Wan DiT) need nothing;
-    with diffusers present the patch in ``pasa_amd.processors.diffusers_patch`` is applied."""
-    try:
-        from . import diffusers_patch
-    except ImportError:
-        return False
-    return diffusers_patch.patch_wan()
+    The reference replaces diffusers' WanTransformerBlock / WanTransformer3DModel
+    forwards for this (svg/models/wan/custom_models.py:23-207); here the model's
+    forward is wrapped instead (``timestep_hook``).  Returns False when diffusers is
+    not importable; callers that pass ``timestep=`` to the processor need neither."""
+    return install_wan()
 
 
 def replace_wan_attention(pipe, height, width, num_frames, first_layers_fp, first_times_fp,
