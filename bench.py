@@ -37,7 +37,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3"])
     ap.add_argument("--cpu-heads", type=int, default=2, help="heads timed for the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
@@ -58,6 +58,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     _lib.load()
     BT, D, H, T = wl.block_size, wl.head_dim, wl.heads, wl.seq_len
+    X = wl.text_tokens          # text segment (c3): dense text rows, exact text keys
     NT = wl.num_blocks()
     ns = ops.num_selected(wl.density, NT)
     flops_k4 = wl.k4_flops(32, ns)
@@ -77,12 +78,12 @@ def main() -> int:
     def step(i):
         e = evs[i]
         e[0].record()
-        st = ops.block_stats(q, k, v, BT, 32)
-        pack = ops.pack_phase2(q, st, BT)
+        st = ops.block_stats(q, k, v, BT, 32, text_tokens=X)
+        pack = ops.pack_phase2(q, st, BT, X)
         e[1].record()
         sel = ops.select_blocks(st, wl.density, scale)
         e[2].record()
-        ops.sparse_attn_packed(q, k, v, pack, sel, scale, BT, out=out)
+        ops.sparse_attn_packed(q, k, v, pack, sel, scale, BT, out=out, text_tokens=X)
         e[3].record()
         last_sel[:] = [sel]
 
@@ -151,7 +152,7 @@ def main() -> int:
         log(f"CPU baseline: oracle on {h} of {H} heads, {cores} threads")
         qc, kc2, vc = make_inputs(wl, seed=args.seed, heads=range(h))
         t0 = time.perf_counter()
-        ref, aux = O.pisa_pg_attention(qc, kc2, vc, wl.density, BT, 32, scale, return_aux=True)
+        ref, aux = O.pisa_pg_attention(qc, kc2, vc, wl.density, BT, 32, scale, return_aux=True, text_tokens=X)
         cpu_s = time.perf_counter() - t0
         cpu_tflops = wl.k4_flops(32, ns) * h / H / cpu_s / 1e12
         cpu = {"value": round(cpu_tflops, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
@@ -166,7 +167,7 @@ def main() -> int:
         same = (torch.sort(gidx, -1).values == torch.sort(aux["idx"].reshape(h, NT, -1), -1).values)
         rows_same = same.all(-1).float().mean().item()
         ref_shared = O.pisa_pg_attention(qc, kc2, vc, wl.density, BT, 32, scale,
-                                         indices=last_sel[0].idx[:, :h].cpu())
+                                         indices=last_sel[0].idx[:, :h].cpu(), text_tokens=X)
         m = O.parity_metrics(out[:, :h].cpu(), ref_shared)
         m_own = O.parity_metrics(out[:, :h].cpu(), ref)
         parity = {"heads": h, "selection_rows_identical": round(rows_same, 6),
@@ -191,9 +192,10 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": f"{args.workload}: {wl.notes}; B=1 H={H} T={T} D={D}, block {BT}, density {wl.density}, "
-                        f"G=32, NS={ns}, NT={NT}; Q pre-scaled by 1/sqrt(128), op scale {scale}",
+                        f"G=32, NS={ns}, NT={NT}; Q pre-scaled by 1/sqrt(128), op scale {scale}"
+                        + (f"; last {X} tokens text (exact keys, dense rows)" if X else ""),
             "heads": H, "seq_len": T, "head_dim": D, "block_size": BT, "density": wl.density,
-            "num_selected": ns, "group_size": 32,
+            "num_selected": ns, "group_size": 32, "text_tokens": X,
         },
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 5),

@@ -12,6 +12,14 @@
  * Tensor layout: q, k, v, o are [B, H, T, D] contiguous, passed as BH = B*H
  * slices of [T, D].  Reference interface cited per entry point; paths are
  * relative to the reference tree (ZHANGWENTAI/PASA).
+ *
+ * Text segment (text_len > 0, head_dim 128 only): the last text_len rows of each
+ * slice are text tokens (HunyuanVideo appends its text last).  Blocks, statistics,
+ * selection and the first-order correction cover the first T - text_len rows; every
+ * video query block also attends to all text keys exactly, and text query rows
+ * attend densely to all T keys.  text_len = 0 is the reference's behaviour (PISA
+ * over all rows as ordinary tokens; group_pisa_attention.py:317, 330-333 document
+ * prompt_token_length but do not use it).
  */
 #ifndef PASA_H_
 #define PASA_H_
@@ -23,7 +31,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 1
+#define PASA_ABI_VERSION 2
 
 typedef enum {
   PASA_OK = 0,
@@ -86,7 +94,8 @@ int pasa_permute(const void* src0, const void* src1, const void* src2,
                  const int32_t* head_is_temporal, int inverse, void* stream);
 
 /* ---- K2: block statistics + per-group first-order moment ------------------
- * For every slice and key block j (NT = ceil(T / block_size), n_j its length):
+ * For every slice and key block j of the first Tv = T - text_len rows
+ * (NT = ceil(Tv / block_size), n_j its length):
  *   qc[j] = mean_t q_t,  kc[j] = mean_t k_t,  vc[j] = sum_t v_t     (fp32 [BH,NT,D])
  *   hnorm[j] = || sum_t (k_t - kc[j]) v_t^T ||_F                        (fp32 [BH,NT])
  *   hgroup[g] = (1/G) * sum_{j in group g, j < NT} H_j                 (fp32 [BH,NG,D,D])
@@ -95,7 +104,7 @@ int pasa_permute(const void* src0, const void* src1, const void* src2,
  *   sqrt at :287) and compute_h_group :291-301. */
 int pasa_block_stats(const void* q, const void* k, const void* v,
                      float* qc, float* kc, float* vc, float* hnorm, float* hgroup,
-                     int64_t bh, int64_t seq_len, int64_t head_dim,
+                     int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
                      int64_t block_size, int64_t group_size, int dtype, void* stream);
 
 /* ---- K3: block scores + deterministic top-k -------------------------------
@@ -143,13 +152,13 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
 int pasa_sparse_attn(const void* q, const void* k, const void* v,
                      const float* kc, const float* vc, const float* hgroup,
                      const int32_t* idx, const uint32_t* selmask, void* o,
-                     double scale, int64_t bh, int64_t seq_len, int64_t head_dim,
+                     double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
                      int64_t block_size, int64_t group_size, int64_t ns,
                      int gamma_literal, int dtype,
                      void* workspace, size_t workspace_bytes, void* stream);
 
-size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t head_dim,
-                                        int64_t block_size, int64_t group_size);
+size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t text_len,
+                                        int64_t head_dim, int64_t block_size, int64_t group_size);
 
 /* The two halves of pasa_sparse_attn, for callers that reuse the packed phase-2
  * operands or time the attention kernel alone.
@@ -159,15 +168,15 @@ size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t hea
  * Replaces: the bf16 stores of kc/vc (group_pisa_attention.py:118-119) and the
  * bf16 cast of h_group at its use (:251). */
 int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
-                     size_t pack_bytes, int64_t bh, int64_t seq_len, int64_t head_dim,
-                     int64_t block_size, int64_t group_size, void* stream);
+                     size_t pack_bytes, int64_t bh, int64_t seq_len, int64_t text_len,
+                     int64_t head_dim, int64_t block_size, int64_t group_size, void* stream);
 
 /* K4 proper on operands packed by pasa_pack_phase2 (same arguments and semantics
  * as pasa_sparse_attn otherwise).
  * Replaces: pisa_pg_fwd_kernel group_pisa_attention.py:135-262. */
 int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack,
                             size_t pack_bytes, const int32_t* idx, const uint32_t* selmask,
-                            void* o, double scale, int64_t bh, int64_t seq_len,
+                            void* o, double scale, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t head_dim, int64_t block_size, int64_t group_size,
                             int64_t ns, int gamma_literal, int dtype, void* stream);
 

@@ -183,8 +183,11 @@ def _bf16(x: torch.Tensor) -> torch.Tensor:
 
 
 def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scale, gamma,
-                   chunk, ref_precision=False):
+                   chunk, ref_precision=False, xk=None, xv=None):
     """One slice.  q,k,v [T,D]; kc,vc [NT,D]; hgroup [NG,D,D]; idx [NT,NS].
+
+    xk, xv: optional [X, D] extra keys/values attended exactly by every query
+    block, after its selected blocks (the text segment of ``text_tokens``).
 
     ref_precision: round where the reference's kernels round (its bf16 storage of
     kc/vc (group_pisa_attention.py:275-277) and of h_group at its use (:251), P and
@@ -214,6 +217,10 @@ def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scal
         Ks = kb[sel].reshape(m, NS * bt, D)
         Vs = vb[sel].reshape(m, NS * bt, D)
         kv = keyvalid[sel].reshape(m, 1, NS * bt)
+        if xk is not None:
+            Ks = torch.cat([Ks, xk[None].expand(m, -1, -1)], dim=1)
+            Vs = torch.cat([Vs, xv[None].expand(m, -1, -1)], dim=1)
+            kv = torch.cat([kv, kv.new_ones(m, 1, xk.shape[0])], dim=2)
         x = c * torch.matmul(Q, Ks.transpose(1, 2))      # :177
         x = x.masked_fill(~kv, float("-inf"))            # :178
         m1 = x.amax(-1)                                  # [m, BT]
@@ -254,7 +261,8 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
                       scale: Optional[float] = None, use_cov_bias: bool = True,
                       noise: Optional[torch.Tensor] = None, gamma: str = "literal",
                       indices: Optional[torch.Tensor] = None, dtype=torch.float32,
-                      chunk: int = 32, return_aux: bool = False, ref_precision: bool = False):
+                      chunk: int = 32, return_aux: bool = False, ref_precision: bool = False,
+                      text_tokens: int = 0):
     """Reference PISA-PG output (:307-398) on the CPU.
 
     q, k, v: [B, H, T, D] (any float dtype, computed in ``dtype``).
@@ -263,11 +271,22 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
     (isolates the attention stage from score rounding).
     gamma: 'literal' (reference: Gamma never rescaled) or 'consistent'.
     ref_precision: emulate the reference's bf16 roundings in the attention stage
-    (the selection stays fp32); see _attention_one."""
+    (the selection stays fp32); see _attention_one.
+    text_tokens: the last ``text_tokens`` rows form a text segment (HunyuanVideo puts
+    its text tokens last, svg/models/hyvideo/attention.py:308-310; the reference
+    documents the intent at group_pisa_attention.py:317, 330-333 but runs PISA over
+    text as ordinary tokens, which is text_tokens=0).  Blocks, statistics, selection
+    and the correction cover the video rows only; every video query block also
+    attends to all text keys exactly, and text query rows attend densely to all keys."""
     B, H, T, D = q.shape
     scale = D ** -0.5 if scale is None else scale
     BH = B * H
+    Tv = T - text_tokens
+    assert 0 <= text_tokens < T
     q3, k3, v3 = (t.reshape(BH, T, D).to(dtype) for t in (q, k, v))
+    if text_tokens:
+        full = (q3, k3, v3)
+        q3, k3, v3 = (t[:, :Tv] for t in full)
     st = block_stats(q3, k3, v3, block_size, dtype)
     hgroup = group_moment(st.hc, group_size)
     NT = st.qc.shape[1]
@@ -281,8 +300,16 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
         idx = indices.reshape(BH, NT, -1).to(torch.int32)
     out = torch.empty(BH, T, D, dtype=dtype)
     for b in range(BH):
-        out[b] = _attention_one(q3[b], k3[b], v3[b], st.kc[b], st.vc[b], hgroup[b], idx[b], st.n,
-                                block_size, group_size, scale, gamma, chunk, ref_precision)
+        xk = xv = None
+        if text_tokens:
+            xk, xv = full[1][b, Tv:], full[2][b, Tv:]
+        out[b, :Tv] = _attention_one(q3[b], k3[b], v3[b], st.kc[b], st.vc[b], hgroup[b], idx[b], st.n,
+                                     block_size, group_size, scale, gamma, chunk, ref_precision, xk, xv)
+        if text_tokens:   # dense text rows, in the same base-2 arithmetic
+            x = (scale * LOG2E) * torch.matmul(full[0][b, Tv:], full[1][b].T)
+            p = torch.exp2(x - x.amax(-1, keepdim=True))
+            o = torch.matmul(p, full[2][b]) / p.sum(-1, keepdim=True)
+            out[b, Tv:] = _bf16(o) if ref_precision else o
     out = out.reshape(B, H, T, D)
     if return_aux:
         return out, dict(stats=st, hgroup=hgroup, scores=scores, idx=idx)
@@ -294,13 +321,20 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
 # ----------------------------------------------------------------------------
 
 def pisa_pg_attention_loop(q, k, v, idx, block_size: int, group_size: int, scale: float,
-                           gamma: str = "literal", dtype=torch.float64):
+                           gamma: str = "literal", dtype=torch.float64, text_tokens: int = 0):
     """Literal restatement of pisa_pg_fwd_kernel's loops for one slice.
 
     q, k, v [T, D]; idx [NT, NS].  Phase 1 walks idx in order (:170-186); phase 2
     walks groups in order with the O(NS) selection re-test (:212-253); Gamma is
-    rescaled only when gamma == 'consistent'.  Intended for tiny inputs."""
+    rescaled only when gamma == 'consistent'.  Intended for tiny inputs.
+    text_tokens: the last rows are text: phase 1 of each video row then walks the
+    text keys one by one; text rows run one online-softmax pass over every key."""
     q, k, v = (t.to(dtype) for t in (q, k, v))
+    T_all = q.shape[0]
+    if text_tokens:
+        qt, kt, vt = q[-text_tokens:], k[-text_tokens:], v[-text_tokens:]
+        kall, vall = k, v
+        q, k, v = q[:-text_tokens], k[:-text_tokens], v[:-text_tokens]
     T, D = q.shape
     bt = block_size
     NT = math.ceil(T / bt)
@@ -325,6 +359,14 @@ def pisa_pg_attention_loop(q, k, v, idx, block_size: int, group_size: int, scale
                 p = torch.exp2(s - new_m)
                 l = l * alpha + p.sum()
                 acc = acc * alpha + sum(p[u] * v[t] for u, t in enumerate(ks))
+                m = new_m
+            for t in range(text_tokens):                   # text keys, exact
+                s_t = c * (qi @ kt[t])
+                new_m = torch.maximum(m, s_t)
+                alpha = torch.exp2(m - new_m)
+                p_t = torch.exp2(s_t - new_m)
+                l = l * alpha + p_t
+                acc = acc * alpha + p_t * vt[t]
                 m = new_m
             g_l = torch.tensor(0.0, dtype=dtype)
             sel = set(idx[I].tolist())
@@ -351,6 +393,21 @@ def pisa_pg_attention_loop(q, k, v, idx, block_size: int, group_size: int, scale
                     g_l = g_l + p[u] * (last_len if j == NT - 1 else bt)
                 acc = acc + (qi @ hg[g]) * (p.sum() * scale)
             out[i] = acc / (l + g_l)
+    if text_tokens:
+        out = torch.cat([out, torch.zeros(text_tokens, D, dtype=dtype)])
+        for i in range(text_tokens):
+            acc = torch.zeros(D, dtype=dtype)
+            l = torch.tensor(0.0, dtype=dtype)
+            m = torch.tensor(float("-inf"), dtype=dtype)
+            for t in range(T_all):
+                s_t = c * (qt[i] @ kall[t])
+                new_m = torch.maximum(m, s_t)
+                alpha = torch.exp2(m - new_m)
+                p_t = torch.exp2(s_t - new_m)
+                l = l * alpha + p_t
+                acc = acc * alpha + p_t * vall[t]
+                m = new_m
+            out[T + i] = acc / l
     return out
 
 

@@ -21,8 +21,8 @@ template <int D, int BT>
 __global__ __launch_bounds__(256, 1) void k2_block_stats(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, float* __restrict__ qc, float* __restrict__ kc,
-    float* __restrict__ vc, float* __restrict__ hnorm, float* __restrict__ hgroup, int T, int NT,
-    int G) {
+    float* __restrict__ vc, float* __restrict__ hnorm, float* __restrict__ hgroup, int T, int Tslice,
+    int NT, int G) {
   constexpr int CH = D / 8;                 // 16-byte chunks per row
   constexpr int ROWS_PER_PASS = 256 / CH;   // rows loaded per pass by the workgroup
   constexpr int PASSES = BT / ROWS_PER_PASS;
@@ -49,7 +49,9 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 
   const int j0 = g * G;
   const int j1 = min(j0 + G, NT);
-  const int64_t slice = (int64_t)bh * T * D;
+  // Slices are Tslice rows apart; only the first T rows (the blocked segment) are
+  // addressable through the buffer resources, so rows >= T read as zero.
+  const int64_t slice = (int64_t)bh * Tslice * D;
   const uint32_t slice_bytes = (uint32_t)T * D * 2u;
   const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
   const rsrc_t kr = make_rsrc(k + slice, slice_bytes);
@@ -211,8 +213,8 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 }
 
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
-                              float* vc, float* hnorm, float* hgroup, int bh, int T, int D, int BT,
-                              int G, hipStream_t stream) {
+                              float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
+                              int BT, int G, hipStream_t stream) {
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + G - 1) / G;
   dim3 grid(NG, bh);
@@ -221,16 +223,16 @@ hipError_t launch_block_stats(const void* q, const void* k, const void* v, float
   auto c = (const uint16_t*)v;
   if (D == 128 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats<128, 128>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
-                       hnorm, hgroup, T, NT, G);
+                       hnorm, hgroup, T, Tslice, NT, G);
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k2_block_stats<128, 64>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
-                       hnorm, hgroup, T, NT, G);
+                       hnorm, hgroup, T, Tslice, NT, G);
   else if (D == 64 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats<64, 128>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
-                       hnorm, hgroup, T, NT, G);
+                       hnorm, hgroup, T, Tslice, NT, G);
   else if (D == 64 && BT == 64)
     hipLaunchKernelGGL((k2_block_stats<64, 64>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
-                       hnorm, hgroup, T, NT, G);
+                       hnorm, hgroup, T, Tslice, NT, G);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -65,6 +65,16 @@ int check_slice_bytes(int64_t seq_len, int64_t head_dim, int64_t elem_bytes) {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The text segment is the last text_len rows of each slice; at least one blocked
+// row must remain.  Only the D = 128 kernels implement it.
+int check_text(int64_t seq_len, int64_t text_len, int64_t head_dim) {
+  if (text_len < 0 || text_len >= seq_len)
+    return fail(PASA_ERR_TEXT_SEGMENT, "text_len=%lld must be in [0, seq_len=%lld)", (long long)text_len, (long long)seq_len);
+  if (text_len > 0 && head_dim != 128)
+    return fail(PASA_ERR_TEXT_SEGMENT, "a text segment needs head_dim 128 (got %lld)", (long long)head_dim);
+  return PASA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -143,8 +153,8 @@ int pasa_permute(const void* src0, const void* src1, const void* src2, void* dst
 }
 
 int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
-                     float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t head_dim,
-                     int64_t block_size, int64_t group_size, int dtype, void* stream) {
+                     float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
+                     int64_t head_dim, int64_t block_size, int64_t group_size, int dtype, void* stream) {
   if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
   if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_block_stats: only bf16 inputs are supported");
   int rc;
@@ -152,10 +162,11 @@ int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, flo
   if ((rc = check_block(block_size))) return rc;
   if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
   if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
+  if ((rc = check_text(seq_len, text_len, head_dim))) return rc;
   if (group_size <= 0 || group_size > 1 << 20) return fail(PASA_ERR_GROUP_SIZE, "group_size %lld must be in [1, 2^20]", (long long)group_size);
-  return launch_status(pasa::launch_block_stats(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh, (int)seq_len,
-                                                (int)head_dim, (int)block_size, (int)group_size,
-                                                (hipStream_t)stream),
+  return launch_status(pasa::launch_block_stats(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh,
+                                                (int)(seq_len - text_len), (int)seq_len, (int)head_dim,
+                                                (int)block_size, (int)group_size, (hipStream_t)stream),
                        "pasa_block_stats");
 }
 
@@ -209,57 +220,59 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
                        "pasa_select_from_scores");
 }
 
-size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t head_dim,
+size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
                                         int64_t block_size, int64_t group_size) {
-  if (bh <= 0 || seq_len <= 0 || (head_dim != 64 && head_dim != 128) ||
+  if (bh <= 0 || seq_len <= 0 || text_len < 0 || text_len >= seq_len || (head_dim != 64 && head_dim != 128) ||
       (block_size != 64 && block_size != 128) || group_size != 32)
     return 0;
-  const int64_t nt = cdiv(seq_len, block_size);
+  const int64_t nt = cdiv(seq_len - text_len, block_size);
   const int64_t ng = cdiv(nt, group_size);
   return (size_t)bh * (size_t)ng * pasa::k4_pack_bytes((int)head_dim, (int)block_size);
 }
 
-static int check_attn_shape(int64_t bh, int64_t seq_len, int64_t head_dim, int64_t block_size,
-                            int64_t group_size) {
+static int check_attn_shape(int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
+                            int64_t block_size, int64_t group_size) {
   int rc;
   if ((rc = check_head_dim(head_dim))) return rc;
   if ((rc = check_block(block_size))) return rc;
   if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
   if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
+  if ((rc = check_text(seq_len, text_len, head_dim))) return rc;
   if (group_size != 32) return fail(PASA_ERR_GROUP_SIZE, "group_size %lld != 32", (long long)group_size);
-  if (8 * bh * cdiv(cdiv(seq_len, block_size), 8) > kMaxI32) return fail(PASA_ERR_OVERFLOW, "grid too large");
+  const int64_t grid = 8 * bh * cdiv(cdiv(seq_len - text_len, block_size), 8) + 8 * cdiv(bh * cdiv(text_len, block_size), 8);
+  if (grid > kMaxI32) return fail(PASA_ERR_OVERFLOW, "grid too large");
   return PASA_OK;
 }
 
-static int check_pack(const void* pack, size_t pack_bytes, int64_t bh, int64_t seq_len, int64_t head_dim,
-                      int64_t block_size, int64_t group_size) {
-  const size_t need = pasa_sparse_attn_workspace_bytes(bh, seq_len, head_dim, block_size, group_size);
+static int check_pack(const void* pack, size_t pack_bytes, int64_t bh, int64_t seq_len, int64_t text_len,
+                      int64_t head_dim, int64_t block_size, int64_t group_size) {
+  const size_t need = pasa_sparse_attn_workspace_bytes(bh, seq_len, text_len, head_dim, block_size, group_size);
   if (!pack || pack_bytes < need)
     return fail(PASA_ERR_WORKSPACE, "phase-2 pack buffer %zu < %zu bytes", pack ? pack_bytes : (size_t)0, need);
   return PASA_OK;
 }
 
 int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack, size_t pack_bytes,
-                     int64_t bh, int64_t seq_len, int64_t head_dim, int64_t block_size,
+                     int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
                      int64_t group_size, void* stream) {
   if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_pack_phase2: NULL pointer");
   int rc;
-  if ((rc = check_attn_shape(bh, seq_len, head_dim, block_size, group_size))) return rc;
-  if ((rc = check_pack(pack, pack_bytes, bh, seq_len, head_dim, block_size, group_size))) return rc;
-  return launch_status(pasa::launch_pack_phase2(kc, vc, hgroup, pack, (int)bh, (int)seq_len, (int)head_dim,
-                                                (int)block_size, (hipStream_t)stream),
+  if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
+  if ((rc = check_pack(pack, pack_bytes, bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
+  return launch_status(pasa::launch_pack_phase2(kc, vc, hgroup, pack, (int)bh, (int)(seq_len - text_len),
+                                                (int)head_dim, (int)block_size, (hipStream_t)stream),
                        "pasa_pack_phase2");
 }
 
 static int check_attn_args(const void* q, const void* k, const void* v, const int32_t* idx,
                            const uint32_t* selmask, const void* o, double scale, int64_t bh,
-                           int64_t seq_len, int64_t head_dim, int64_t block_size, int64_t group_size,
-                           int64_t ns, int gamma_literal, int dtype) {
+                           int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
+                           int64_t group_size, int64_t ns, int gamma_literal, int dtype) {
   if (!q || !k || !v || !idx || !selmask || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
   if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_sparse_attn: only bf16 inputs are supported");
   int rc;
-  if ((rc = check_attn_shape(bh, seq_len, head_dim, block_size, group_size))) return rc;
-  const int64_t nt = cdiv(seq_len, block_size);
+  if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
+  const int64_t nt = cdiv(seq_len - text_len, block_size);
   if (ns < 1 || ns > nt) return fail(PASA_ERR_NUM_SELECTED, "ns=%lld not in [1, %lld]", (long long)ns, (long long)nt);
   if (nt > INT64_MAX / bh / ns) return fail(PASA_ERR_OVERFLOW, "bh*NT*ns overflows");
   if (!std::isfinite(scale) || !(scale > 0.0)) return fail(PASA_ERR_BAD_ARG, "scale must be finite and > 0");
@@ -269,35 +282,36 @@ static int check_attn_args(const void* q, const void* k, const void* v, const in
 
 int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack, size_t pack_bytes,
                             const int32_t* idx, const uint32_t* selmask, void* o, double scale, int64_t bh,
-                            int64_t seq_len, int64_t head_dim, int64_t block_size, int64_t group_size,
-                            int64_t ns, int gamma_literal, int dtype, void* stream) {
+                            int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
+                            int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* stream) {
   int rc;
-  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, head_dim, block_size, group_size,
-                            ns, gamma_literal, dtype)))
+  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, head_dim, block_size,
+                            group_size, ns, gamma_literal, dtype)))
     return rc;
-  if ((rc = check_pack(pack, pack_bytes, bh, seq_len, head_dim, block_size, group_size))) return rc;
+  if ((rc = check_pack(pack, pack_bytes, bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
   return launch_status(pasa::launch_sparse_attn(q, k, v, pack, idx, selmask, o, (float)scale, (int)bh,
-                                                (int)seq_len, (int)head_dim, (int)block_size, (int)ns,
-                                                gamma_literal, (hipStream_t)stream),
+                                                (int)(seq_len - text_len), (int)text_len, (int)head_dim,
+                                                (int)block_size, (int)ns, gamma_literal, (hipStream_t)stream),
                        "pasa_sparse_attn");
 }
 
 int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* kc, const float* vc,
                      const float* hgroup, const int32_t* idx, const uint32_t* selmask, void* o,
-                     double scale, int64_t bh, int64_t seq_len, int64_t head_dim, int64_t block_size,
-                     int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
+                     int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype,
+                     void* workspace, size_t workspace_bytes, void* stream) {
   if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
   int rc;
-  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, head_dim, block_size, group_size,
-                            ns, gamma_literal, dtype)))
+  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, head_dim, block_size,
+                            group_size, ns, gamma_literal, dtype)))
     return rc;
-  if ((rc = check_pack(workspace, workspace_bytes, bh, seq_len, head_dim, block_size, group_size))) return rc;
-  if ((rc = pasa_pack_phase2(kc, vc, hgroup, workspace, workspace_bytes, bh, seq_len, head_dim, block_size,
-                             group_size, stream)))
+  if ((rc = check_pack(workspace, workspace_bytes, bh, seq_len, text_len, head_dim, block_size, group_size)))
+    return rc;
+  if ((rc = pasa_pack_phase2(kc, vc, hgroup, workspace, workspace_bytes, bh, seq_len, text_len, head_dim,
+                             block_size, group_size, stream)))
     return rc;
   return pasa_sparse_attn_packed(q, k, v, workspace, workspace_bytes, idx, selmask, o, scale, bh, seq_len,
-                                 head_dim, block_size, group_size, ns, gamma_literal, dtype, stream);
+                                 text_len, head_dim, block_size, group_size, ns, gamma_literal, dtype, stream);
 }
 
 }  // extern "C"

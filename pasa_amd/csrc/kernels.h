@@ -14,9 +14,10 @@ hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* 
                           void* d2, int ntens, int bh, int S, int F, int P, int ctx, int row_bytes,
                           const int32_t* head_is_temporal, int inverse, hipStream_t stream);
 
+// T: rows of the blocked segment; Tslice: rows per slice (T plus any text rows).
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
-                              float* vc, float* hnorm, float* hgroup, int bh, int T, int D, int BT,
-                              int G, hipStream_t stream);
+                              float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
+                              int BT, int G, hipStream_t stream);
 
 hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,
                          float scale, int use_cov_bias, float* scores, int bh, int NT, int D,
@@ -30,9 +31,11 @@ size_t k4_pack_bytes(int D, int BT);  // per (slice, group) phase-2 pack image
 hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
                               int bh, int T, int D, int BT, hipStream_t stream);
 
+// T: rows of the blocked (video) segment; text: rows of the text segment that
+// follows it in each slice (slices are T + text rows apart).
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
-                              int bh, int T, int D, int BT, int NS, int gamma_literal,
+                              int bh, int T, int text, int D, int BT, int NS, int gamma_literal,
                               hipStream_t stream);
 
 }  // namespace pasa

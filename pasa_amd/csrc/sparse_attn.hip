@@ -518,7 +518,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
                         const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
                         const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o,
                         float scale, float c, int T, int NT, int NG, int NW, int xcd_chunk,
-                        int gamma_literal) {
+                        int gamma_literal, int text, int n_text_wg, int nbh) {
   using C = K4D<BT>;
   using PK = typename C::PK;
   constexpr int D = 128;
@@ -526,22 +526,42 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   __shared__ __attribute__((aligned(1024))) unsigned char Ks[C::KBUF];
   __shared__ __attribute__((aligned(1024))) unsigned char Vs[C::VBUF];
 
+  // Each slice holds T blocked (video) rows followed by `text` text rows.  The first
+  // n_text_wg workgroups (a multiple of 8) each own one tile of text query rows and
+  // attend densely to every key; they are the longest-running ones, so they go first.
+  // The rest own one query block of the video rows; wg & 7 names their XCD, and each
+  // XCD takes a contiguous run of a slice's query blocks (shared K/V tiles in its L2).
   const int wg = blockIdx.x;
-  const int xcd = wg & 7;
-  const int slot = wg >> 3;
-  const int bh = slot / xcd_chunk;
-  const int qb = xcd * xcd_chunk + (slot - bh * xcd_chunk);
-  if (qb >= NT) return;
+  const bool dense = wg < n_text_wg;
+  int bh, qb, qrow0, row_limit;
+  if (dense) {
+    const int qtiles = (text + BT - 1) / BT;
+    bh = wg / qtiles;
+    if (bh >= nbh) return;  // padding of the text range to a multiple of 8
+    qb = 0;
+    qrow0 = T + (wg - bh * qtiles) * BT;
+    row_limit = T + text;
+  } else {
+    const int w = wg - n_text_wg;
+    const int xcd = w & 7;
+    const int slot = w >> 3;
+    bh = slot / xcd_chunk;
+    qb = xcd * xcd_chunk + (slot - bh * xcd_chunk);
+    if (qb >= NT) return;
+    qrow0 = qb * BT;
+    row_limit = T;
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5;
   const int l32 = lane & 31;
-  const int64_t slice = (int64_t)bh * T * D;
-  const int qrow = qb * BT + wave * 32 + l32;
+  const int Ttot = T + text;
+  const int64_t slice = (int64_t)bh * Ttot * D;
+  const int qrow = qrow0 + wave * 32 + l32;
 
-  const uint32_t slice_bytes = (uint32_t)T * D * 2u;
+  const uint32_t slice_bytes = (uint32_t)Ttot * D * 2u;
   const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
 
   bf16x8_t qf[D / 16];
@@ -582,16 +602,17 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const u32x4_t vd = make_rsrc_words(v + slice, slice_bytes);
   const uint32_t ks_lds = lds_addr(Ks);
   const uint32_t vs_lds = lds_addr(Vs);
-  auto load_k = [&](int blk) {
-    const uint32_t soff = (uint32_t)blk * BT * 256u;
+  // A tile is BT key rows starting at row `row0` of the slice (rows past the slice read as zero).
+  auto load_k = [&](int row0) {
+    const uint32_t soff = (uint32_t)row0 * 256u;
 #pragma unroll
     for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
       for (int n = 0; n < BT / 16; ++n)
         dma_load16_lds(kd, ks_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256, k_lane[vw] + 16 * n * 256, soff);
   };
-  auto load_v = [&](int blk) {
-    const uint32_t soff = (uint32_t)blk * BT * 256u;
+  auto load_v = [&](int row0) {
+    const uint32_t soff = (uint32_t)row0 * 256u;
 #pragma unroll
     for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
@@ -614,7 +635,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
                ((4 * (et ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
 
   int wsel = 0;
-  uint32_t bits = NW > 0 ? mrow[0] : 0u;
+  uint32_t bits = (!dense && NW > 0) ? mrow[0] : 0u;
   auto next_selected = [&]() -> int {
     while (bits == 0u) {
       if (++wsel >= NW) return -1;
@@ -624,15 +645,40 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     bits &= bits - 1u;
     return j;
   };
+  // Exact tiles in visiting order: a video query block takes its selected blocks in
+  // ascending order, then the text rows; a text query tile takes every row of the slice.
+  // Returns the tile's first row (-1 when done) and its number of valid rows in nv.
+  int tt = 0;
+  const int text_tiles = (text + BT - 1) / BT;
+  const int all_tiles = (Ttot + BT - 1) / BT;
+  auto next_tile = [&](int& nv) -> int {
+    if (dense) {
+      if (tt >= all_tiles) return -1;
+      const int r = tt++ * BT;
+      nv = min(BT, Ttot - r);
+      return r;
+    }
+    const int j = next_selected();
+    if (j >= 0) {
+      nv = min(BT, T - j * BT);
+      return j * BT;
+    }
+    if (tt >= text_tiles) return -1;
+    const int r = tt++ * BT;
+    nv = min(BT, text - r);
+    return T + r;
+  };
 
   // ---------------- Phase 1 ------------------------------------------------------
-  int blk = next_selected();
+  int nv_cur = 0;
+  int blk = next_tile(nv_cur);
   if (blk >= 0) {
     load_k(blk);
     load_v(blk);
   }
   while (blk >= 0) {
-    const int nxt = next_selected();
+    int nv_nxt = 0;
+    const int nxt = next_tile(nv_nxt);
     wait_vmcnt<C::TILE_LOADS>();  // this wave's K_blk loads landed (V_blk may be in flight)
     barrier_lds_reads_done();     // ... and every wave's
 
@@ -653,7 +699,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     barrier_lds_reads_done();  // every wave: V_blk landed, K_blk reads done
     if (nxt >= 0) load_k(nxt);
 
-    const int nvalid = min(BT, T - blk * BT);
+    const int nvalid = nv_cur;
     if (nvalid < BT) {
 #pragma unroll
       for (int mt = 0; mt < BT / 32; ++mt)
@@ -702,6 +748,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     barrier_lds_reads_done();  // every wave is done reading V_blk
     if (nxt >= 0) load_v(nxt);
     blk = nxt;
+    nv_cur = nv_nxt;
   }
 
   // ---------------- Phase 2 ------------------------------------------------------
@@ -709,7 +756,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const u32x4_t pd = make_rsrc_words(pack + (int64_t)bh * NG * PK::BYTES, (uint32_t)(NG * PK::BYTES));
   const unsigned char* Pvt = Vs + PK::VT_OFF;
   const int pv_base = PadTile<kGroup>::frag_base(l32, h);
-  for (int g = 0; g < NG; ++g) {
+  const int ng_run = dense ? 0 : NG;  // text rows have no correction term
+  for (int g = 0; g < ng_run; ++g) {
     const int nin = min(kGroup, NT - g * kGroup);
     const uint32_t inrange = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
     const uint32_t approx = inrange & ~mrow[g];
@@ -805,7 +853,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   }
 
   const float denom = halves_sum(l_run) + halves_sum(g_run);
-  if (qrow < T) {
+  if (qrow < row_limit) {
     uint16_t* orow = o + slice + (int64_t)qrow * D;
 #pragma unroll
     for (int et = 0; et < D / 32; ++et)
@@ -849,13 +897,16 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
 
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
-                              int bh, int T, int D, int BT, int NS, int gamma_literal,
+                              int bh, int T, int text, int D, int BT, int NS, int gamma_literal,
                               hipStream_t stream) {
+  if (text > 0 && D != 128) return hipErrorInvalidValue;  // the text segment is a D = 128 feature
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + kGroup - 1) / kGroup;
   const int NW = (NT + 31) / 32;
   const int xcd_chunk = (NT + 7) / 8;
-  dim3 grid(8 * bh * xcd_chunk);
+  const int n_text_wg = text > 0 ? (bh * ((text + BT - 1) / BT) + 7) / 8 * 8 : 0;
+  dim3 grid(n_text_wg + 8 * bh * xcd_chunk);
+  dim3 grid_video(8 * bh * xcd_chunk);
   const float c = scale * kLog2e;
   auto a = (const uint16_t*)q;
   auto b = (const uint16_t*)k;
@@ -863,14 +914,14 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
   auto pk = (const unsigned char*)pack;
   auto oo = (uint16_t*)o;
 #define PASA_K4_LAUNCH(DD, BB)                                                                   \
-  hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
+  hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid_video, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
                      b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
   if (D == 128 && BT == 128)
     hipLaunchKernelGGL((k4_sparse_attn_dma<128>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal);
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, n_text_wg, bh);
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k4_sparse_attn_dma<64>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal);
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, n_text_wg, bh);
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
   else if (D == 64 && BT == 64)

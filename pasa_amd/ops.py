@@ -64,14 +64,15 @@ class BlockStats:
 
 
 def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int = 64,
-                group_size: int = GROUP_SIZE) -> BlockStats:
+                group_size: int = GROUP_SIZE, text_tokens: int = 0) -> BlockStats:
     """Block means of Q/K, block sums of V, ||H_j||_F and the group mean of H_j.
 
     Replaces fused_chunk_reduce (reference :268-288; hc is never materialised)
-    followed by compute_h_group (:291-301)."""
+    followed by compute_h_group (:291-301).  With ``text_tokens`` the blocks cover
+    the first T - text_tokens rows only."""
     _check_device(q, k, v)
     B, H, T, D = q.shape
-    NT = math.ceil(T / block_size)
+    NT = math.ceil((T - text_tokens) / block_size)
     NG = math.ceil(NT / group_size)
     f32 = dict(device=q.device, dtype=torch.float32)
     qc = torch.empty(B, H, NT, D, **f32)
@@ -80,8 +81,8 @@ def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: i
     hnorm = torch.empty(B, H, NT, **f32)
     hgroup = torch.empty(B, H, NG, D, D, **f32)
     _lib.call("pasa_block_stats", q.data_ptr(), k.data_ptr(), v.data_ptr(), qc.data_ptr(),
-              kc.data_ptr(), vc.data_ptr(), hnorm.data_ptr(), hgroup.data_ptr(), B * H, T, D,
-              block_size, group_size, _DTYPES.get(q.dtype, -1), _stream(q))
+              kc.data_ptr(), vc.data_ptr(), hnorm.data_ptr(), hgroup.data_ptr(), B * H, T, int(text_tokens),
+              D, block_size, group_size, _DTYPES.get(q.dtype, -1), _stream(q))
     return BlockStats(qc, kc, vc, hnorm, hgroup)
 
 
@@ -134,23 +135,23 @@ def select_from_scores(scores: torch.Tensor, ns: int) -> Selection:
     return Selection(idx, selmask, scores, int(ns))
 
 
-def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64) -> torch.Tensor:
+def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_tokens: int = 0) -> torch.Tensor:
     """bf16 phase-2 operands (kbar, V^T, Hbar^T) per (slice, group), as K4 stages them in LDS."""
     B, H, T, D = q.shape
     lib = _lib.load()
-    nbytes = int(lib.pasa_sparse_attn_workspace_bytes(B * H, T, D, block_size, GROUP_SIZE))
+    nbytes = int(lib.pasa_sparse_attn_workspace_bytes(B * H, T, int(text_tokens), D, block_size, GROUP_SIZE))
     if nbytes == 0:
         raise ValueError(f"unsupported shape for the gfx950 kernels: D={D}, block_size={block_size}")
     pack = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
     _check_device(stats.kc, stats.vc, stats.hgroup)
     _lib.call("pasa_pack_phase2", stats.kc.data_ptr(), stats.vc.data_ptr(), stats.hgroup.data_ptr(),
-              pack.data_ptr(), pack.numel(), B * H, T, D, block_size, GROUP_SIZE, _stream(q))
+              pack.data_ptr(), pack.numel(), B * H, T, int(text_tokens), D, block_size, GROUP_SIZE, _stream(q))
     return pack
 
 
 def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: torch.Tensor,
                        sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
-                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       out: Optional[torch.Tensor] = None, text_tokens: int = 0) -> torch.Tensor:
     """K4 on operands from ``pack_phase2``."""
     _check_device(q, k, v, pack)
     if gamma not in ("literal", "consistent"):
@@ -160,18 +161,20 @@ def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: 
     _check_device(o)
     _lib.call("pasa_sparse_attn_packed", q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(),
               pack.numel(), sel.idx.data_ptr(), sel.selmask.data_ptr(), o.data_ptr(), float(scale),
-              B * H, T, D, block_size, GROUP_SIZE, sel.ns, int(gamma == "literal"),
+              B * H, T, int(text_tokens), D, block_size, GROUP_SIZE, sel.ns, int(gamma == "literal"),
               _DTYPES.get(q.dtype, -1), _stream(q))
     return o
 
 
 def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockStats,
                 sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                out: Optional[torch.Tensor] = None, text_tokens: int = 0) -> torch.Tensor:
     """Exact attention over the selected blocks plus the per-group first-order
-    correction of the rest (reference pisa_pg_fwd_kernel :135-262)."""
-    pack = pack_phase2(q, stats, block_size)
-    return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out)
+    correction of the rest (reference pisa_pg_fwd_kernel :135-262); with
+    ``text_tokens``, the text keys are exact for every video query block and the
+    text rows are dense."""
+    pack = pack_phase2(q, stats, block_size, text_tokens)
+    return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out, text_tokens)
 
 
 def pisa_pg_attention(
@@ -188,6 +191,7 @@ def pisa_pg_attention(
     *,
     noise: Optional[torch.Tensor] = None,
     gamma: str = "literal",
+    text_tokens: int = 0,
 ):
     """PISA with per-group first-order correction (drop-in for reference :307-398).
 
@@ -198,17 +202,21 @@ def pisa_pg_attention(
     ``noise`` (fp32 [B,H,NT]) to make it reproducible, else it is drawn on the
     device from torch's default generator like the reference's ``randn_like``.
     ``gamma='consistent'`` rescales the zero-order denominator with the running max
-    (the reference's literal form does not)."""
+    (the reference's literal form does not).
+    ``text_tokens``: the last rows are a text segment (HunyuanVideo's layout):
+    blocks, selection and correction cover the video rows, every video query block
+    attends to the text keys exactly and text rows attend densely to all keys.  The
+    default 0 is the reference's behaviour (text as ordinary tokens)."""
     B, H, T, D = q.shape
     if group_size != GROUP_SIZE:
         raise ValueError(f"the gfx950 kernels use group_size={GROUP_SIZE}")
     scale = D ** -0.5 if scale is None else scale
-    NT = math.ceil(T / block_size)
-    stats = block_stats(q, k, v, block_size, group_size)
+    NT = math.ceil((T - text_tokens) / block_size)
+    stats = block_stats(q, k, v, block_size, group_size, text_tokens)
     if use_random and use_cov_bias and noise is None:
         noise = torch.randn(B, H, NT, device=q.device, dtype=torch.float32)
     sel = select_blocks(stats, density, scale, use_cov_bias, noise if use_cov_bias else None)
     if verbose:
         print(f"NT={NT}, N_GROUPS={stats.hgroup.shape[2]}, GROUP_SIZE={group_size}")
         print(f"top_k={sel.ns}, density={density}")
-    return sparse_attn(q, k, v, stats, sel, scale, block_size, gamma)
+    return sparse_attn(q, k, v, stats, sel, scale, block_size, gamma, text_tokens=text_tokens)

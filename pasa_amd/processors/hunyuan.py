@@ -23,6 +23,8 @@ Notes on the reference:
   build; that setting raises ``NotImplementedError``.
 * The sparse call passes the whole joint sequence, text tokens included, to
   ``pisa_pg_attention`` with block_size=64 (:680): text tokens are ordinary tokens.
+  ``text_segment = True`` (class attribute) instead treats the trailing
+  ``context_length`` tokens as a text segment (``pisa_pg_attention(text_tokens=...)``).
 Left out (not on the hot path): sample_mse / flex-attention SVG masks (:382-411).
 """
 from __future__ import annotations
@@ -254,6 +256,10 @@ class Hunyuan_PASA_Processor(Hunyuan_SVGAttn_Processor2_0):
     use_random = True
     block_size = 64        # the reference's call site passes block_size=64 (:680)
     logging_file = None
+    # False (the reference): the text tokens are ordinary tokens of the sparse call.
+    # True: the last context_length tokens are a text segment (exact text keys for
+    # every video query block, dense text rows); needs head_dim 128.
+    text_segment = False
 
     def __init__(self, layer_idx):
         super().__init__(layer_idx)
@@ -281,8 +287,9 @@ class Hunyuan_PASA_Processor(Hunyuan_SVGAttn_Processor2_0):
         if not self.use_group:
             raise NotImplementedError("use_group=False selects piecewise_sparse_attention "
                                       "(svg/kernels/triton/pisa_attention.py), which this build does not provide")
+        extra = {"text_tokens": context_length} if self.text_segment else {}
         out = pisa_pg_attention(query.contiguous(), key.contiguous(), value.contiguous(), density=density,
-                                block_size=self.block_size, use_random=self.use_random)
+                                block_size=self.block_size, use_random=self.use_random, **extra)
         return out.reshape(cfg, num_heads, seq_len, dim)
 
 

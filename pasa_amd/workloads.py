@@ -51,17 +51,23 @@ class Workload:
         return self.head_dim ** -0.5 if self.scale is None else self.scale
 
     def num_blocks(self) -> int:
-        return math.ceil(self.seq_len / self.block_size)
+        """Key blocks of the blocked segment: the video rows (text rows, when present,
+        are a separate dense segment)."""
+        return math.ceil(self.video_tokens / self.block_size)
 
     def k4_flops(self, group_size: int = 32, ns: Optional[int] = None) -> float:
-        """Algorithmic K4 FLOPs: BH*[4*D*BT^2*NT*NS + NT*NG*(4*BT*G*D + 2*BT*D^2)]."""
+        """Algorithmic K4 FLOPs: BH*[4*D*BT^2*NT*NS + NT*NG*(4*BT*G*D + 2*BT*D^2)] + F_text,
+        F_text = 4*D*(Tv*X + X*(Tv + X))*BH for X text tokens (video rows x text keys
+        and dense text rows)."""
         nt = self.num_blocks()
         ng = math.ceil(nt / group_size)
         if ns is None:
             ns = min(max(1, int(self.density * nt)), nt)
         bt, d = self.block_size, self.head_dim
         bh = self.batch * self.heads
-        return bh * (4.0 * d * bt * bt * nt * ns + nt * ng * (4.0 * bt * group_size * d + 2.0 * bt * d * d))
+        tv, x = self.video_tokens, self.text_tokens
+        f_text = 4.0 * d * (tv * x + x * (tv + x)) * bh
+        return bh * (4.0 * d * bt * bt * nt * ns + nt * ng * (4.0 * bt * group_size * d + 2.0 * bt * d * d)) + f_text
 
 
 A1_PRESCALE = 128 ** -0.5  # "pre-scaled by 1/sqrt(128)": folded into Q, op scale 1.0

@@ -93,16 +93,17 @@ def test_permute_validation(lib, kw, code, msg):
 
 def stats(lib, **kw):
     a = dict(q=FAKE, k=FAKE, v=FAKE, qc=FAKE, kc=FAKE, vc=FAKE, hn=FAKE, hg=FAKE, bh=4, T=1000,
-             D=128, BT=128, G=32, dtype=0)
+             text=0, D=128, BT=128, G=32, dtype=0)
     a.update(kw)
     return lib.pasa_block_stats(a["q"], a["k"], a["v"], a["qc"], a["kc"], a["vc"], a["hn"], a["hg"],
-                                a["bh"], a["T"], a["D"], a["BT"], a["G"], a["dtype"], None)
+                                a["bh"], a["T"], a["text"], a["D"], a["BT"], a["G"], a["dtype"], None)
 
 
 @pytest.mark.parametrize("kw,code", [
     (dict(q=None), -1), (dict(hg=None), -1), (dict(dtype=2), -7), (dict(dtype=1), -7),
     (dict(D=96), -3), (dict(BT=32), -4), (dict(T=0), -2), (dict(bh=-1), -2), (dict(G=0), -12),
     (dict(T=1 << 31), -6), (dict(T=(1 << 24) - 100), -6),
+    (dict(text=-1), -10), (dict(text=1000), -10), (dict(text=10, D=64), -10),
 ])
 def test_block_stats_validation(lib, kw, code):
     assert stats(lib, **kw) == code
@@ -141,11 +142,11 @@ def test_select_from_scores_validation(lib):
 
 def attn(lib, **kw):
     a = dict(q=FAKE, k=FAKE, v=FAKE, kc=FAKE, vc=FAKE, hg=FAKE, idx=FAKE, mask=FAKE, o=FAKE, scale=0.1,
-             bh=2, T=1000, D=128, BT=128, G=32, ns=2, lit=1, dtype=0, ws=FAKE, wsb=1 << 30)
+             bh=2, T=1000, text=0, D=128, BT=128, G=32, ns=2, lit=1, dtype=0, ws=FAKE, wsb=1 << 30)
     a.update(kw)
     return lib.pasa_sparse_attn(a["q"], a["k"], a["v"], a["kc"], a["vc"], a["hg"], a["idx"], a["mask"],
-                                a["o"], a["scale"], a["bh"], a["T"], a["D"], a["BT"], a["G"], a["ns"],
-                                a["lit"], a["dtype"], a["ws"], a["wsb"], None)
+                                a["o"], a["scale"], a["bh"], a["T"], a["text"], a["D"], a["BT"], a["G"],
+                                a["ns"], a["lit"], a["dtype"], a["ws"], a["wsb"], None)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -153,7 +154,8 @@ def attn(lib, **kw):
     (dict(BT=256), -4), (dict(G=16), -12), (dict(ns=0), -5), (dict(ns=9), -5),
     (dict(scale=0.0), -9), (dict(scale=-1.0), -9), (dict(scale=float("nan")), -9),
     (dict(lit=2), -9), (dict(ws=None), -8), (dict(wsb=10), -8), (dict(T=0), -2),
-    (dict(T=(1 << 24) - 100), -6),
+    (dict(T=(1 << 24) - 100), -6), (dict(text=1000), -10), (dict(text=-3), -10),
+    (dict(text=100, D=64), -10), (dict(text=200, ns=8), -5),
 ])
 def test_sparse_attn_validation(lib, kw, code):
     assert attn(lib, **kw) == code
@@ -162,26 +164,32 @@ def test_sparse_attn_validation(lib, kw, code):
 
 def test_packed_entry_validation(lib):
     pk = lib.pasa_pack_phase2
-    need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 128, 128, 32)
-    assert pk(FAKE, FAKE, FAKE, FAKE, need - 1, 2, 1000, 128, 128, 32, None) == -8
-    assert pk(None, FAKE, FAKE, FAKE, need, 2, 1000, 128, 128, 32, None) == -1
-    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 128, 128, 16, None) == -12
+    need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 0, 128, 128, 32)
+    assert pk(FAKE, FAKE, FAKE, FAKE, need - 1, 2, 1000, 0, 128, 128, 32, None) == -8
+    assert pk(None, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 32, None) == -1
+    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 16, None) == -12
+    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 1000, 128, 128, 32, None) == -10
     f = lib.pasa_sparse_attn_packed
-    args = [FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, 2, 1000, 128, 128, 32, 2, 1, 0, None]
+    args = [FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, 2, 1000, 0, 128, 128, 32, 2, 1, 0, None]
     bad = list(args); bad[4] = 0
     assert f(*bad) == -8
-    bad = list(args); bad[14] = 100
+    bad = list(args); bad[15] = 100
     assert f(*bad) == -5
-    bad = list(args); bad[16] = 2
+    bad = list(args); bad[17] = 2
     assert f(*bad) == -7
+    bad = list(args); bad[11] = -1
+    assert f(*bad) == -10
 
 
 def test_workspace_bytes(lib):
     f = lib.pasa_sparse_attn_workspace_bytes
     # c2: 40 slices, NT = 591, NG = 19 groups of a 53248-byte phase-2 LDS image
-    assert f(40, 75600, 128, 128, 32) == 40 * 19 * 53248
-    assert f(40, 75600, 128, 128, 16) == 0
-    assert f(1, 1024, 64, 64, 32) > 0
+    assert f(40, 75600, 0, 128, 128, 32) == 40 * 19 * 53248
+    assert f(40, 75600, 0, 128, 128, 16) == 0
+    assert f(1, 1024, 0, 64, 64, 32) > 0
+    # c3: 118800 video rows (NT 929, NG 30) + 256 text rows
+    assert f(24, 118800 + 256, 256, 128, 128, 32) == 24 * 30 * 53248
+    assert f(24, 1000, 1000, 128, 128, 32) == 0
 
 
 def test_last_error_cleared_on_success(lib):

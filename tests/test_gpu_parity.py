@@ -236,7 +236,7 @@ def test_full_density_equals_dense_attention(device):
 def check_end_to_end(o, q, k, v, wl, gpu_idx, noise=None, what=""):
     """Whole-op parity with the oracle's own selection; selection differences must be near ties."""
     ref, aux = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, noise=noise,
-                                   return_aux=True)
+                                   return_aux=True, text_tokens=wl.text_tokens)
     H, NT = q.shape[1], wl.num_blocks()
     oidx = aux["idx"].reshape(1, H, NT, -1)
     scores = aux["scores"].reshape(1, H, NT, NT)
@@ -255,7 +255,8 @@ def check_end_to_end(o, q, k, v, wl, gpu_idx, noise=None, what=""):
         m = O.parity_metrics(o.cpu(), ref)
         say(f"[E2E] {what} all rows: cos={m['cos']:.7f} max_abs/rms={m['max_abs_over_rms']:.3e}")
         assert m["cos"] >= COS_MIN
-        keep = (~differ).repeat_interleave(wl.block_size, -1)[..., : q.shape[2]]     # [1, H, T]
+        keep = (~differ).repeat_interleave(wl.block_size, -1)[..., : wl.video_tokens]   # [1, H, Tv]
+        keep = torch.cat([keep, keep.new_ones(*keep.shape[:-1], wl.text_tokens)], -1)  # text rows: dense
         rms = float(ref.double().pow(2).mean().sqrt())
         e = (o.cpu().double() - ref.double()).abs()
         excess = float(((e - O.bf16_ulp(ref.double())).clamp_min(0)).amax(-1)[keep].max())
@@ -291,3 +292,63 @@ def test_end_to_end_c2_full_shape(device):
     for h in (0, wl.heads - 1):
         sl = slice(h, h + 1)
         check_end_to_end(oc[:, sl], q[:, sl], k[:, sl], v[:, sl], wl, idx[:, sl], None, f"c2 head {h}")
+
+
+# ------------------------------------------------------------ text segment --
+
+TEXT_CASES = [
+    # heads, grid, text, BT, density, gamma
+    (2, (3, 10, 20), 40, 128, 0.4, "literal"),      # last video block 88 rows; one partial text tile
+    (1, (5, 13, 17), 256, 64, 0.2, "literal"),      # BT 64 kernel; four text tiles
+    (2, (3, 10, 20), 300, 128, 0.3, "consistent"),  # three text tiles, the last partial
+]
+
+
+def text_inputs(heads, grid, text, BT, density, seed):
+    wl = small_workload(WORKLOADS["c3"], heads=heads, grid=grid, block_size=BT, density=density,
+                        text_tokens=text, prescale=1.0, scale=None)
+    return wl, make_inputs(wl, seed=seed, dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("heads,grid,text,BT,density,gamma", TEXT_CASES)
+def test_text_segment_shared_selection(device, heads, grid, text, BT, density, gamma):
+    wl, (q, k, v) = text_inputs(heads, grid, text, BT, density, seed=4)
+    T, Tv = wl.seq_len, wl.video_tokens
+    say(f"[text] heads={heads} Tv={Tv} text={text} BT={BT} density={density} gamma={gamma}")
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    scale = 128 ** -0.5
+    st = ops.block_stats(qd, kd, vd, BT, 32, text_tokens=text)
+    ref_st = O.block_stats(*(t[0, :, :Tv].double() for t in (q, k, v)), BT, dtype=torch.float64)
+    assert st.qc.shape[2] == wl.num_blocks()
+    torch.testing.assert_close(st.kc[0].cpu().double(), ref_st.kc, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(st.vc[0].cpu().double(), ref_st.vc, rtol=1e-5, atol=1e-4)
+    sel = ops.select_blocks(st, density, scale)
+    o = ops.sparse_attn(qd, kd, vd, st, sel, scale, BT, gamma, text_tokens=text)
+    idx = sel.idx.cpu()
+    ref = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, gamma=gamma, indices=idx, text_tokens=text)
+    rp = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, gamma=gamma, indices=idx, text_tokens=text,
+                             ref_precision=True)
+    floor = O.parity_metrics(rp, ref)
+    check_parity(o.cpu(), ref, f"text {Tv}+{text} BT{BT} {gamma}", floor)
+    check_parity(o.cpu()[..., Tv:, :], ref[..., Tv:, :], "text rows (dense)")
+
+
+def test_text_segment_full_density_equals_dense_attention(device):
+    wl, (q, k, v) = text_inputs(2, (3, 10, 20), 100, 128, 1.0, seed=5)
+    say("[text] density 1.0 with a text segment vs softmax attention")
+    o = ops.pisa_pg_attention(q.to(device), k.to(device), v.to(device), density=1.0, block_size=128,
+                              text_tokens=100)
+    ref = O.dense_attention(q.double(), k.double(), v.double(), O.effective_scale(128 ** -0.5))
+    check_parity(o.cpu(), ref, "text density=1")
+
+
+def test_end_to_end_c3_one_head_text_segment(device):
+    wl = small_workload(WORKLOADS["c3"], heads=1, grid=(9, 45, 80))
+    say(f"[E2E] c3 layout, 1 head, {wl.video_tokens} video + {wl.text_tokens} text tokens")
+    q, k, v = make_inputs(wl, seed=0)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    o = ops.pisa_pg_attention(qd, kd, vd, density=wl.density, block_size=wl.block_size, scale=wl.op_scale,
+                              text_tokens=wl.text_tokens)
+    st = ops.block_stats(qd, kd, vd, wl.block_size, 32, text_tokens=wl.text_tokens)
+    idx = ops.select_blocks(st, wl.density, wl.op_scale).idx.cpu()
+    check_end_to_end(o, q, k, v, wl, idx, None, "c3 one head")

@@ -169,3 +169,53 @@ def test_parity_metrics():
     assert m["cos"] == pytest.approx(1.0) and m["max_abs"] == 0.0
     m = O.parity_metrics(a + torch.tensor([0.0, 0.0, 0.1]), a)
     assert m["max_abs"] == pytest.approx(0.1, abs=1e-6)
+
+
+# ------------------------------------------------------------ text segment --
+
+@pytest.mark.parametrize("T,text,bt,G,density,gamma", [
+    (100, 12, 16, 2, 0.34, "literal"), (100, 12, 16, 2, 0.34, "consistent"),
+    (90, 17, 8, 3, 0.25, "literal"), (64, 40, 16, 1, 0.5, "literal")])
+def test_text_segment_closed_form_matches_sequential_loop(T, text, bt, G, density, gamma):
+    q, k, v = rand_qkv(1, 2, T, 6, seed=T + text, scale=1.5)
+    s = 6 ** -0.5
+    out, aux = O.pisa_pg_attention(q, k, v, density, bt, G, s, gamma=gamma, dtype=f64, return_aux=True,
+                                   text_tokens=text)
+    assert aux["idx"].shape[1] == -(-(T - text) // bt)      # blocks cover the video rows only
+    for b in range(2):
+        ref = O.pisa_pg_attention_loop(q[0, b], k[0, b], v[0, b], aux["idx"][b], bt, G, s, gamma,
+                                       text_tokens=text)
+        torch.testing.assert_close(out[0, b], ref, rtol=1e-10, atol=1e-10)
+
+
+def test_text_segment_full_density_is_softmax_attention():
+    q, k, v = rand_qkv(1, 2, 77, 8, seed=5)
+    out = O.pisa_pg_attention(q, k, v, 1.0, 16, 2, 8 ** -0.5, dtype=f64, text_tokens=13)
+    ref = O.dense_attention(q, k, v, O.effective_scale(8 ** -0.5))
+    torch.testing.assert_close(out, ref, rtol=1e-10, atol=1e-10)
+
+
+def test_text_rows_are_dense_and_video_rows_ignore_text_queries():
+    q, k, v = rand_qkv(1, 1, 80, 8, seed=6)
+    s = 8 ** -0.5
+    out = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, s, dtype=f64, text_tokens=16)
+    ref = O.dense_attention(q, k, v, O.effective_scale(s))
+    torch.testing.assert_close(out[..., 64:, :], ref[..., 64:, :], rtol=1e-10, atol=1e-10)
+    q2 = q.clone()
+    q2[..., 64:, :] = torch.randn(16, 8, dtype=f64)           # text queries do not touch video rows
+    out2 = O.pisa_pg_attention(q2, k, v, 0.25, 16, 2, s, dtype=f64, text_tokens=16)
+    torch.testing.assert_close(out2[..., :64, :], out[..., :64, :], rtol=0, atol=0)
+
+
+def test_text_segment_with_negligible_text_keys_is_video_only_pisa():
+    # Text keys far below every score (exp2 underflows to 0) change nothing for video rows.
+    q, k, v = rand_qkv(1, 1, 96, 8, seed=7)
+    k = k.clone()
+    q = q.clone()
+    q[..., :, 0] = q[..., :, 0].abs() + 1.0            # every query has a positive first coordinate
+    k[..., 80:, :] = 0.0
+    k[..., 80:, 0] = -1e4                              # text keys: q.k <= -1e4
+    s = 8 ** -0.5
+    out = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, s, dtype=f64, text_tokens=16)
+    ref = O.pisa_pg_attention(q[..., :80, :], k[..., :80, :], v[..., :80, :], 0.25, 16, 2, s, dtype=f64)
+    torch.testing.assert_close(out[..., :80, :], ref, rtol=1e-12, atol=1e-12)

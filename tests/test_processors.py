@@ -223,6 +223,13 @@ def test_hunyuan_pasa_dispatch(monkeypatch, hy_config):
     # sparse: nearest calibrated key of 500 is 488 (factor 0.9239564591192239)
     hy_config(5).attention_core_logic(q, q, q, torch.tensor([500]), 5, cu)
     assert rec.calls == [dict(density=0.2 * 0.9239564591192239, block_size=64, use_random=True)]
+    hy_config.text_segment = True
+    try:
+        hy_config(5).attention_core_logic(q, q, q, torch.tensor([500]), 5, cu)
+    finally:
+        hy_config.text_segment = False
+    assert rec.calls[-1] == dict(density=0.2 * 0.9239564591192239, block_size=64, use_random=True,
+                                 text_tokens=3)
 
 
 def test_hunyuan_pasa_use_group_false_raises(monkeypatch, hy_config):
