@@ -510,7 +510,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // are not drained (a fenced __syncthreads would wait for them).  It is used only
 // where this wave's preceding LDS reads have been consumed by MFMAs, i.e. have
 // completed, and where the next LDS writes are direct loads issued after it.
-__device__ __forceinline__ void barrier_lds_reads_done() { __builtin_amdgcn_s_barrier(); }
+__device__ __forceinline__ void barrier_lds_reads_done() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads have returned
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");       // no LDS access moves across the barrier
+}
+
+// Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 template <int BT>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
@@ -694,18 +702,34 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + mt * 32 * 256));
         sacc[mt] = mfma32(a, qf[ks], sacc[mt]);
       }
+    // Keep 8 fragment reads in flight: each MFMA consumes a read issued 8 MFMAs
+    // (~256 cycles) earlier, which covers the LDS latency.
+    {
+      constexpr int N = (D / 16) * (BT / 32);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+#pragma unroll
+      for (int i = 0; i < N - 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    }
 
-    wait_vmcnt<0>();           // V_blk landed
-    barrier_lds_reads_done();  // every wave: V_blk landed, K_blk reads done
+    barrier_lds_reads_done();  // every wave is done reading K_blk
     if (nxt >= 0) load_k(nxt);
 
     const int nvalid = nv_cur;
     if (nvalid < BT) {
+      // key mt*32 + 8(r>>2) + 4h + (r&3) is past the tile's rows iff its h-free part
+      // reaches lim; comparing against immediates keeps no per-key constants live.
+      const int lim = nvalid - 4 * h;
 #pragma unroll
       for (int mt = 0; mt < BT / 32; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (mt * 32 + mfma32_row(r, h) >= nvalid) sacc[mt][r] = -INFINITY;
+          if (mt * 32 + 8 * (r >> 2) + (r & 3) >= lim) sacc[mt][r] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -736,6 +760,13 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       }
       pf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
     }
+    // V_blk is waited for only now, so its load overlaps S and the softmax; the
+    // K_{blk+1} loads issued after it may stay in flight.
+    if (nxt >= 0)
+      wait_vmcnt<C::TILE_LOADS>();
+    else
+      wait_vmcnt<0>();
+    barrier_lds_reads_done();  // every wave's part of V_blk landed
 #pragma unroll
     for (int s = 0; s < BT / 16; ++s)
 #pragma unroll
@@ -745,6 +776,19 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         const bf16x8_t a = __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
         oacc[et] = mfma32(a, pf[s], oacc[et]);
       }
+    // Same read-ahead for the transposing V reads (two per MFMA): 4 MFMAs of operands in flight.
+    {
+      constexpr int N = (BT / 16) * (D / 32);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 1);
+#pragma unroll
+      for (int i = 0; i < N - 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+    }
     barrier_lds_reads_done();  // every wave is done reading V_blk
     if (nxt >= 0) load_v(nxt);
     blk = nxt;
@@ -757,26 +801,48 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const unsigned char* Pvt = Vs + PK::VT_OFF;
   const int pv_base = PadTile<kGroup>::frag_base(l32, h);
   const int ng_run = dense ? 0 : NG;  // text rows have no correction term
-  for (int g = 0; g < ng_run; ++g) {
+  // Groups with at least one unselected in-range block, in ascending order.
+  auto approx_of = [&](int g) -> uint32_t {
     const int nin = min(kGroup, NT - g * kGroup);
     const uint32_t inrange = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
-    const uint32_t approx = inrange & ~mrow[g];
-    if (approx == 0u) continue;
-
-    barrier_lds_reads_done();  // previous readers of both buffers are done
+    return inrange & ~mrow[g];
+  };
+  auto next_group = [&](int g) -> int {
+    for (++g; g < ng_run; ++g)
+      if (approx_of(g) != 0u) return g;
+    return -1;
+  };
+  // A group's pack is two parts: kbar + V^T (part 2, into Vs) and Hbar^T (into Ks).
+  // Part 2 of the next group loads while this group's Hbar^T product runs, and the
+  // next Hbar^T loads while the next group's scores and P.V^ run.
+  constexpr int HT_LOADS = PK::HT_BYTES / 1024 / C::WAVES;
+  constexpr int P2_LOADS = PK::PART2 / 1024 / C::WAVES;
+  auto load_part2 = [&](int g) {
     const uint32_t gsoff = (uint32_t)(g * PK::BYTES);
 #pragma unroll
-    for (int n = 0; n < PK::HT_BYTES / 1024 / C::WAVES; ++n) {
-      const int kb = n * C::WAVES + wave;  // 1 KB piece of Hbar^T
-      dma_load16_lds(pd, ks_lds + kb * 1024, (uint32_t)(kb * 1024 + lane * 16), gsoff);
-    }
-#pragma unroll
-    for (int n = 0; n < PK::PART2 / 1024 / C::WAVES; ++n) {
+    for (int n = 0; n < P2_LOADS; ++n) {
       const int kb = n * C::WAVES + wave;
       dma_load16_lds(pd, vs_lds + kb * 1024, (uint32_t)(PK::HT_BYTES + kb * 1024 + lane * 16), gsoff);
     }
-    wait_vmcnt<0>();
-    barrier_lds_reads_done();
+  };
+  auto load_ht = [&](int g) {
+    const uint32_t gsoff = (uint32_t)(g * PK::BYTES);
+#pragma unroll
+    for (int n = 0; n < HT_LOADS; ++n) {
+      const int kb = n * C::WAVES + wave;  // 1 KB piece of Hbar^T
+      dma_load16_lds(pd, ks_lds + kb * 1024, (uint32_t)(kb * 1024 + lane * 16), gsoff);
+    }
+  };
+  int g = next_group(-1);
+  if (g >= 0) {  // phase 1 ended with a barrier after the last reads of Ks and Vs
+    load_part2(g);
+    load_ht(g);
+  }
+  while (g >= 0) {
+    const int gn = next_group(g);
+    const uint32_t approx = approx_of(g);
+    wait_vmcnt<HT_LOADS>();    // this wave's part 2 of group g landed (Hbar^T may be in flight)
+    barrier_lds_reads_done();  // ... and every wave's
 
     f32x16_t sb;
 #pragma unroll
@@ -833,6 +899,14 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
             as_bf16x8(lds_ld<uint4>(Pvt, pv_base + et * 32 * PadTile<kGroup>::ROW_BYTES + s * 16));
         oacc[et] = mfma32(a, pbf[s], oacc[et]);
       }
+    barrier_lds_reads_done();  // every wave is done reading part 2 of group g
+    if (gn >= 0) load_part2(gn);
+    if (gn >= 0)
+      wait_vmcnt<P2_LOADS>();  // Hbar^T of group g landed (part 2 of gn may be in flight)
+    else
+      wait_vmcnt<0>();
+    barrier_lds_reads_done();
+
     f32x16_t racc[D / 32];
 #pragma unroll
     for (int et = 0; et < D / 32; ++et)
@@ -850,6 +924,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int et = 0; et < D / 32; ++et)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[et][r] = fmaf(racc[et][r], f, oacc[et][r]);
+    barrier_lds_reads_done();  // every wave is done reading Hbar^T of group g
+    if (gn >= 0) load_ht(gn);
+    g = gn;
   }
 
   const float denom = halves_sum(l_run) + halves_sum(g_run);
