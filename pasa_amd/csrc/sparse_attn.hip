@@ -126,6 +126,10 @@ __host__ __device__ __forceinline__ constexpr int xor_tile_byte(int row, int col
   return row * 256 + ((((col >> 3) ^ row) & 15) << 4) + (col & 7) * 2;
 }
 
+// One workgroup per (group, slice).  Every output element is written once, as part of
+// a 16-byte chunk: Hbar^T goes through LDS (coalesced fp32 reads of Hbar rows, column
+// reads from a padded tile), kbar rows are read as 32-byte runs, V^T columns with the
+// token index fastest across lanes.  Rounding is round-to-nearest-even, as everywhere.
 template <int BT>
 __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
                                                    const float* __restrict__ vc,
@@ -133,32 +137,78 @@ __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
                                                    unsigned char* __restrict__ pack, int NT, int NG) {
   using P = K4DPack<BT>;
   constexpr int D = 128;
+  constexpr int HS = D + 1;  // padded row of the fp32 Hbar tile
+  __shared__ float hs[D * HS];
   const int g = blockIdx.x;
   const int bh = blockIdx.y;
+  const int tid = threadIdx.x;
   unsigned char* out = pack + ((int64_t)bh * NG + g) * P::BYTES;
   const float* kb = kc + (int64_t)bh * NT * D;
   const float* vb = vc + (int64_t)bh * NT * D;
   const float* hb = hgroup + ((int64_t)bh * NG + g) * D * D;
-  for (int u = threadIdx.x; u < D * D; u += 256) {
-    const int d = u / D;  // Hbar[d][e] row-major in, Hbar^T[e][d] out
-    const int e = u - d * D;
-    *(uint16_t*)(out + xor_tile_byte(e, d)) = (uint16_t)f32_to_bf16_bits(hb[u]);
+#pragma unroll 4
+  for (int it = 0; it < D * D / 4 / 256; ++it) {
+    const int idx = it * 256 + tid;
+    const int d = idx >> 5;
+    const int e4 = (idx & 31) * 4;
+    const float4 x = *(const float4*)(hb + d * D + e4);
+    hs[d * HS + e4 + 0] = x.x;
+    hs[d * HS + e4 + 1] = x.y;
+    hs[d * HS + e4 + 2] = x.z;
+    hs[d * HS + e4 + 3] = x.w;
   }
+  // kbar: rows m (block of the group) x 16 chunks of 8 features, XOR layout.
   unsigned char* part2 = out + P::HT_BYTES;
-  for (int u = threadIdx.x; u < kGroup * D; u += 256) {
-    const int m = u / D;
-    const int d = u - m * D;
+#pragma unroll
+  for (int it = 0; it < kGroup * D / 8 / 256; ++it) {
+    const int qi = it * 256 + tid;
+    const int m = qi >> 4;
+    const int cc = qi & 15;
     const int jj = g * kGroup + m;
-    const float x = jj < NT ? kb[(int64_t)jj * D + d] : 0.f;
-    *(uint16_t*)(part2 + P::KB_OFF + xor_tile_byte(m, d)) = (uint16_t)f32_to_bf16_bits(x);
+    float f[8];
+    if (jj < NT) {
+      const float4 x0 = *(const float4*)(kb + (int64_t)jj * D + cc * 8);
+      const float4 x1 = *(const float4*)(kb + (int64_t)jj * D + cc * 8 + 4);
+      f[0] = x0.x; f[1] = x0.y; f[2] = x0.z; f[3] = x0.w;
+      f[4] = x1.x; f[5] = x1.y; f[6] = x1.z; f[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = 0.f;
+    }
+    const uint4 w = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                               pack_bf16x2(f[6], f[7]));
+    *(uint4*)(part2 + P::KB_OFF + xor_tile_byte(m, cc * 8)) = w;
   }
-  for (int u = threadIdx.x; u < D * kGroup; u += 256) {
-    const int m = u % kGroup;
-    const int e = u / kGroup;
-    const int jj = g * kGroup + m;
-    const float x = jj < NT ? vb[(int64_t)jj * D + e] : 0.f;
-    *(uint16_t*)(part2 + P::VT_OFF + PadTile<kGroup>::elem_byte(e, tok_perm(m))) =
-        (uint16_t)f32_to_bf16_bits(x);
+  // V^T: feature rows e x 4 chunks of 8 (permuted) tokens of the padded tile.
+#pragma unroll
+  for (int it = 0; it < D * kGroup / 8 / 256; ++it) {
+    const int qi = it * 256 + tid;
+    const int e = qi & (D - 1);
+    const int cc = qi >> 7;
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = tok_perm(cc * 8 + i);  // tok_perm is its own inverse
+      const int jj = g * kGroup + m;
+      f[i] = jj < NT ? vb[(int64_t)jj * D + e] : 0.f;
+    }
+    const uint4 w = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                               pack_bf16x2(f[6], f[7]));
+    *(uint4*)(part2 + P::VT_OFF + PadTile<kGroup>::chunk_byte(e, cc)) = w;
+  }
+  __syncthreads();
+  // Hbar^T: row e, chunk cc holds Hbar[8 cc .. 8 cc + 7][e].
+#pragma unroll 2
+  for (int it = 0; it < D * D / 8 / 256; ++it) {
+    const int qi = it * 256 + tid;
+    const int e = qi >> 4;
+    const int cc = qi & 15;
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = hs[(cc * 8 + i) * HS + e];
+    const uint4 w = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                               pack_bf16x2(f[6], f[7]));
+    *(uint4*)(out + xor_tile_byte(e, cc * 8)) = w;
   }
 }
 
