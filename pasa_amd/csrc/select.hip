@@ -91,32 +91,99 @@ __device__ __forceinline__ uint64_t topk_key(float s, int j) {
   return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - (uint32_t)j);
 }
 
-// One wavefront per (slice, query block).  Dynamic LDS: NTP * 8 bytes.
-__global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, int NT, int NTP,
-                                              int NS, int NW, int32_t* __restrict__ idx,
+// Inclusive prefix sum over the 64 lanes of a wavefront.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t t = __shfl_up(x, d, 64);
+    if (lane >= d) x += t;
+  }
+  return x;
+}
+
+// One wavefront per (slice, query block); the row's keys live in registers, KPL per
+// lane (key i*64 + lane).  The NS-th largest key is found exactly by an MSB-first
+// radix select over the 64-bit keys (8 bits per pass; keys are unique because they
+// carry the block index), the NS keys at or above it are compacted into LDS and
+// sorted there in descending order.  Dynamic LDS: NSP * 8 bytes (NSP = pow2 >= NS).
+template <int KPL>
+__global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, int NT, int NS, int NSP,
+                                              int NW, int32_t* __restrict__ idx,
                                               uint32_t* __restrict__ selmask) {
-  extern __shared__ uint64_t keys[];
+  extern __shared__ uint64_t sel[];
+  __shared__ uint32_t hist[256];
   __shared__ uint32_t words[kMaxSelectBlocks / 32];
   const int row = blockIdx.x;
   const int bh = blockIdx.y;
   const int lane = threadIdx.x;
   const float* srow = scores + ((int64_t)bh * NT + row) * NT;
 
-  for (int i = lane; i < NTP; i += 64) keys[i] = i < NT ? topk_key(srow[i], i) : 0ull;
+  uint64_t key[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int j = i * 64 + lane;
+    key[i] = j < NT ? topk_key(srow[j], j) : 0ull;  // 0 is below every real key
+  }
   for (int w = lane; w < NW; w += 64) words[w] = 0u;
+
+  uint64_t prefix = 0ull, mask = 0ull;
+  uint32_t need = (uint32_t)NS;  // rank of the threshold among the keys matching prefix
+#pragma unroll 1
+  for (int shift = 56; shift >= 0; shift -= 8) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) hist[4 * lane + t] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+      if (i * 64 + lane < NT && (key[i] & mask) == prefix) atomicAdd(&hist[(uint32_t)(key[i] >> shift) & 255u], 1u);
+    __syncthreads();
+    uint32_t hb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) hb[t] = hist[4 * lane + t];
+    const uint32_t s = hb[0] + hb[1] + hb[2] + hb[3];
+    const uint32_t incl = wave_incl_scan(s);
+    const uint32_t total = __shfl(incl, 63, 64);
+    uint32_t cum = total - incl;  // candidates in the bins of higher lanes
+    int found = -1;
+    uint32_t above = 0u;
+#pragma unroll
+    for (int t = 3; t >= 0; --t) {
+      if (found < 0 && cum < need && need <= cum + hb[t]) {
+        found = 4 * lane + t;
+        above = cum;
+      }
+      cum += hb[t];
+    }
+    const uint64_t hit = __ballot(found >= 0);
+    const int src = __ffsll((long long)hit) - 1;
+    const uint32_t bin = (uint32_t)__shfl(found, src, 64);
+    need -= (uint32_t)__shfl((int)above, src, 64);
+    prefix |= (uint64_t)bin << shift;
+    mask |= 0xffull << shift;
+  }
+  // prefix is now the NS-th largest key: select the keys >= it.
+  uint32_t cnt = 0u;
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) cnt += (i * 64 + lane < NT && key[i] >= prefix) ? 1u : 0u;
+  uint32_t pos = wave_incl_scan(cnt) - cnt;
+#pragma unroll
+  for (int i = 0; i < KPL; ++i)
+    if (i * 64 + lane < NT && key[i] >= prefix) sel[pos++] = key[i];
+  for (int i = NS + lane; i < NSP; i += 64) sel[i] = 0ull;
   __syncthreads();
 
-  for (int kk = 2; kk <= NTP; kk <<= 1) {
+  for (int kk = 2; kk <= NSP; kk <<= 1) {
     for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-      for (int p = lane; p < (NTP >> 1); p += 64) {
+      for (int p = lane; p < (NSP >> 1); p += 64) {
         const int i = ((p & ~(jj - 1)) << 1) | (p & (jj - 1));
         const int l = i + jj;
-        const uint64_t a = keys[i];
-        const uint64_t b = keys[l];
+        const uint64_t a = sel[i];
+        const uint64_t b = sel[l];
         const bool desc = (i & kk) == 0;
         if (desc ? (a < b) : (a > b)) {
-          keys[i] = b;
-          keys[l] = a;
+          sel[i] = b;
+          sel[l] = a;
         }
       }
       __syncthreads();
@@ -125,7 +192,7 @@ __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, 
 
   int32_t* irow = idx + ((int64_t)bh * NT + row) * NS;
   for (int i = lane; i < NS; i += 64) {
-    const int j = (int)(0xffffffffu - (uint32_t)(keys[i] & 0xffffffffull));
+    const int j = (int)(0xffffffffu - (uint32_t)(sel[i] & 0xffffffffull));
     irow[i] = j;
     atomicOr(&words[j >> 5], 1u << (j & 31));
   }
@@ -145,13 +212,27 @@ hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, c
 
 hipError_t launch_topk(const float* scores, int bh, int NT, int NS, int32_t* idx,
                        uint32_t* selmask, hipStream_t stream) {
-  int NTP = 1;
-  while (NTP < NT) NTP <<= 1;
-  if (NTP < 2) NTP = 2;
+  int NSP = 1;
+  while (NSP < NS) NSP <<= 1;
+  if (NSP < 2) NSP = 2;
   const int NW = (NT + 31) / 32;
   dim3 grid(NT, bh);
-  hipLaunchKernelGGL(k3_topk, grid, dim3(64), (size_t)NTP * sizeof(uint64_t), stream, scores, NT,
-                     NTP, NS, NW, idx, selmask);
+  const size_t lds = (size_t)NSP * sizeof(uint64_t);
+#define PASA_TOPK(K) \
+  hipLaunchKernelGGL((k3_topk<K>), grid, dim3(64), lds, stream, scores, NT, NS, NSP, NW, idx, selmask)
+  if (NT <= 64 * 4)
+    PASA_TOPK(4);
+  else if (NT <= 64 * 8)
+    PASA_TOPK(8);
+  else if (NT <= 64 * 16)
+    PASA_TOPK(16);
+  else if (NT <= 64 * 32)
+    PASA_TOPK(32);
+  else if (NT <= 64 * 64)
+    PASA_TOPK(64);
+  else
+    return hipErrorInvalidValue;
+#undef PASA_TOPK
   return hipGetLastError();
 }
 
