@@ -212,6 +212,220 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
     }
 }
 
+// D = 128, BT = 128: the same statistics with the block loads overlapped.  K and V
+// tiles go straight into double-buffered LDS (direct loads, 256-byte rows with 16-byte
+// chunk c of row r at c ^ 4(r & 3)); Q rows go to registers.  Block j+1's loads are in
+// flight while block j is reduced.  H_j = K^T V reads both MFMA operands with the
+// transposing ds_read_b64_tr_b16 (K^T as A, V as B; the same token order in both).
+__global__ __launch_bounds__(256, 1) void k2_block_stats_dma(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, float* __restrict__ qc, float* __restrict__ kc,
+    float* __restrict__ vc, float* __restrict__ hnorm, float* __restrict__ hgroup, int T, int Tslice,
+    int NT, int G) {
+  constexpr int D = 128;
+  constexpr int BT = 128;
+  constexpr int TILE = BT * 256;
+  __shared__ __attribute__((aligned(1024))) unsigned char Kb[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char Vb[2 * TILE];
+  __shared__ float red_sum[4][3 * D];
+  __shared__ float colstat[3 * D];
+  __shared__ float red_norm[4];
+
+  const int g = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+  const int dq = (wave >> 1) * 64;
+  const int eq = (wave & 1) * 64;
+  const int j0 = g * G;
+  const int j1 = min(j0 + G, NT);
+
+  const int64_t slice = (int64_t)bh * Tslice * D;
+  const uint32_t slice_bytes = (uint32_t)T * D * 2u;  // rows >= T read as zero
+  const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
+  const u32x4_t kd = make_rsrc_words(k + slice, slice_bytes);
+  const u32x4_t vd = make_rsrc_words(v + slice, slice_bytes);
+  const uint32_t kb_lds = lds_addr(Kb);
+  const uint32_t vb_lds = lds_addr(Vb);
+
+  // Direct loads: load n of wave w covers rows 16n + 4w + lane/16 (chunk lane % 16).
+  const int lrow = lane >> 4;
+  const int lch = lane & 15;
+  const uint32_t t_lane = (uint32_t)((4 * wave + lrow) * 256 + ((lch ^ (4 * lrow)) << 4));
+  auto load_kv = [&](int buf, int j) {
+    const uint32_t soff = (uint32_t)j * BT * 256u;
+#pragma unroll
+    for (int n = 0; n < BT / 16; ++n)
+      dma_load16_lds(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, t_lane + 16 * n * 256, soff);
+#pragma unroll
+    for (int n = 0; n < BT / 16; ++n)
+      dma_load16_lds(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, t_lane + 16 * n * 256, soff);
+  };
+  // Q: thread t holds rows 16p + t/16, 16-byte chunk t % 16, for p < 8.
+  const int prow = tid >> 4;
+  const int pc = tid & 15;
+  auto load_q = [&](uint4 (&qv)[BT / 16], int j) {
+#pragma unroll
+    for (int p = 0; p < BT / 16; ++p)
+      qv[p] = buf_load16(qr, ((uint32_t)(j * BT + 16 * p + prow) * D + pc * 8) * 2u);
+  };
+
+  // Transposing operand reads: lane gets feature 32 ft + l32, tokens 4h + {0..3} (lo)
+  // and 8 + 4h + {0..3} (hi) of token step s.
+  const int g16 = lane >> 4;
+  const int i16 = lane & 15;
+  int tofs[D / 32];
+#pragma unroll
+  for (int ft = 0; ft < D / 32; ++ft)
+    tofs[ft] = (4 * (g16 >> 1) + (i16 >> 2)) * 256 +
+               ((4 * (ft ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
+  auto frag = [&](const unsigned char* base, int ft, int s) {
+    const uint2 lo = lds_read_tr16(base, tofs[ft] + s * 16 * 256);
+    const uint2 hi = lds_read_tr16(base, tofs[ft] + s * 16 * 256 + 8 * 256);
+    return __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
+  };
+
+  f32x16_t gacc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) gacc[a][b][r] = 0.f;
+
+  uint4 qv[BT / 16], qn[BT / 16];
+  if (j0 < j1) {
+    load_kv(0, j0);
+    load_q(qv, j0);
+  }
+  for (int j = j0; j < j1; ++j) {
+    const int buf = (j - j0) & 1;
+    const int n = min(BT, T - j * BT);
+    wait_vmcnt<0>();           // block j's K, V (LDS) and Q (registers) landed
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // every wave's parts; block j-1's readers of buffer buf^1 done
+    asm volatile("" ::: "memory");
+    if (j + 1 < j1) {
+      load_kv(buf ^ 1, j + 1);
+      load_q(qn, j + 1);
+    }
+    const unsigned char* Kt = Kb + buf * TILE;
+    const unsigned char* Vt = Vb + buf * TILE;
+
+    // Column sums: Q from registers, K and V from the LDS tiles (same rows and chunk).
+    float ps[3][8];
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps[a][i] = 0.f;
+#pragma unroll
+    for (int p = 0; p < BT / 16; ++p) {
+      const int r = 16 * p + prow;
+      const int off = r * 256 + ((pc ^ (4 * (r & 3))) << 4);
+      float f[8];
+      unpack8(qv[p], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps[0][i] += f[i];
+      unpack8(lds_ld<uint4>(Kt, off), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps[1][i] += f[i];
+      unpack8(lds_ld<uint4>(Vt, off), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps[2][i] += f[i];
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x = ps[a][i];
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        ps[a][i] = x;
+      }
+    if (lane < 16) {
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) red_sum[wave][a * D + lane * 8 + i] = ps[a][i];
+    }
+    __syncthreads();
+    const float nf = (float)n;
+    for (int idx = tid; idx < 3 * D; idx += 256) {
+      float sm = ((red_sum[0][idx] + red_sum[1][idx]) + red_sum[2][idx]) + red_sum[3][idx];
+      const int a = idx / D;
+      const int d = idx - a * D;
+      if (a < 2) sm = sm / nf;
+      colstat[idx] = sm;
+      float* dst = a == 0 ? qc : (a == 1 ? kc : vc);
+      dst[((int64_t)bh * NT + j) * D + d] = sm;
+    }
+    __syncthreads();
+
+    // H_j quadrant = K^T V (rows >= n are zero in both tiles).
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < BT / 16; ++s2) {
+      bf16x8_t af[2], bfr[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) af[mt] = frag(Kt, dq / 32 + mt, s2);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) bfr[nt] = frag(Vt, eq / 32 + nt, s2);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(af[mt], bfr[nt], acc[mt][nt]);
+    }
+    float nrm = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int e = eq + nt * 32 + l32;
+        const float vsum = colstat[2 * D + e];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = dq + mt * 32 + mfma32_row(r, h);
+          const float hv = acc[mt][nt][r] - colstat[D + d] * vsum;
+          nrm += hv * hv;
+          gacc[mt][nt][r] += hv;
+        }
+      }
+    nrm = wave_sum(nrm);
+    if (lane == 0) red_norm[wave] = nrm;
+    __syncthreads();
+    if (tid == 0) {
+      const float sn = ((red_norm[0] + red_norm[1]) + red_norm[2]) + red_norm[3];
+      hnorm[(int64_t)bh * NT + j] = sqrtf(sn);
+    }
+#pragma unroll
+    for (int p = 0; p < BT / 16; ++p) qv[p] = qn[p];
+  }
+
+  const int NG = (NT + G - 1) / G;
+  float* hg = hgroup + ((int64_t)bh * NG + g) * D * D;
+  const float Gf = (float)G;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int e = eq + nt * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = dq + mt * 32 + mfma32_row(r, h);
+        hg[d * D + e] = gacc[mt][nt][r] / Gf;
+      }
+    }
+}
+
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
                               int BT, int G, hipStream_t stream) {
@@ -222,8 +436,8 @@ hipError_t launch_block_stats(const void* q, const void* k, const void* v, float
   auto b = (const uint16_t*)k;
   auto c = (const uint16_t*)v;
   if (D == 128 && BT == 128)
-    hipLaunchKernelGGL((k2_block_stats<128, 128>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
-                       hnorm, hgroup, T, Tslice, NT, G);
+    hipLaunchKernelGGL(k2_block_stats_dma, grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm, hgroup,
+                       T, Tslice, NT, G);
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k2_block_stats<128, 64>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
                        hnorm, hgroup, T, Tslice, NT, G);

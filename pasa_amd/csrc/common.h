@@ -97,6 +97,13 @@ __device__ __forceinline__ void dma_load16_lds(u32x4_t rsrc, uint32_t lds_addr, 
                : "memory");
 }
 
+// vmcnt-only wait (expcnt / lgkmcnt left unconstrained), gfx9 s_waitcnt encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 __device__ __forceinline__ u32x4_t make_rsrc_words(const void* base, uint32_t bytes) {
   const uint64_t a = (uint64_t)base;
   return (u32x4_t){(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};

@@ -549,12 +549,6 @@ struct K4D {
   static_assert(TILE_LOADS == 8, "load schedule");
 };
 
-// vmcnt-only wait (expcnt / lgkmcnt left unconstrained), gfx9 s_waitcnt encoding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // Workgroup barrier without a memory fence, so in-flight direct-to-LDS tile loads
 // are not drained (a fenced __syncthreads would wait for them).  It is used only
