@@ -20,6 +20,13 @@
  * attend densely to all T keys.  text_len = 0 is the reference's behaviour (PISA
  * over all rows as ordinary tokens; group_pisa_attention.py:317, 330-333 document
  * prompt_token_length but do not use it).
+ * Text padding (pasa_sparse_attn*'s text_valid, 0 <= text_valid <= text_len): only
+ * the first text_valid text rows are the prompt, the rest padding.  As in the
+ * reference's dense HunyuanVideo path (cu_seqlens [0, valid, T],
+ * svg/models/hyvideo/attention.py:314-322), the sequence splits into two segments
+ * that attend only within themselves: video rows and prompt rows see the video
+ * rows and the prompt keys, padding rows see the padding keys.  text_valid =
+ * text_len means no padding.
  */
 #ifndef PASA_H_
 #define PASA_H_
@@ -31,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 2
+#define PASA_ABI_VERSION 3
 
 typedef enum {
   PASA_OK = 0,
@@ -152,7 +159,8 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
 int pasa_sparse_attn(const void* q, const void* k, const void* v,
                      const float* kc, const float* vc, const float* hgroup,
                      const int32_t* idx, const uint32_t* selmask, void* o,
-                     double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
+                     double scale, int64_t bh, int64_t seq_len, int64_t text_len,
+                     int64_t text_valid, int64_t head_dim,
                      int64_t block_size, int64_t group_size, int64_t ns,
                      int gamma_literal, int dtype,
                      void* workspace, size_t workspace_bytes, void* stream);
@@ -177,8 +185,8 @@ int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void
 int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack,
                             size_t pack_bytes, const int32_t* idx, const uint32_t* selmask,
                             void* o, double scale, int64_t bh, int64_t seq_len, int64_t text_len,
-                            int64_t head_dim, int64_t block_size, int64_t group_size,
-                            int64_t ns, int gamma_literal, int dtype, void* stream);
+                            int64_t text_valid, int64_t head_dim, int64_t block_size,
+                            int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -262,7 +262,7 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
                       noise: Optional[torch.Tensor] = None, gamma: str = "literal",
                       indices: Optional[torch.Tensor] = None, dtype=torch.float32,
                       chunk: int = 32, return_aux: bool = False, ref_precision: bool = False,
-                      text_tokens: int = 0):
+                      text_tokens: int = 0, text_valid: Optional[int] = None):
     """Reference PISA-PG output (:307-398) on the CPU.
 
     q, k, v: [B, H, T, D] (any float dtype, computed in ``dtype``).
@@ -277,12 +277,20 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
     documents the intent at group_pisa_attention.py:317, 330-333 but runs PISA over
     text as ordinary tokens, which is text_tokens=0).  Blocks, statistics, selection
     and the correction cover the video rows only; every video query block also
-    attends to all text keys exactly, and text query rows attend densely to all keys."""
+    attends to all text keys exactly, and text query rows attend densely to all keys.
+    text_valid: the first text_valid text tokens are real, the rest padding (HunyuanVideo
+    pads its prompt; its dense path attends block-diagonally over cu_seqlens
+    [0, Tv + text_valid, T], svg/models/hyvideo/attention.py:315-323).  Video rows then
+    take exact keys only from the valid text rows, valid text rows attend densely to
+    [0, Tv + text_valid) and padding rows to the padding segment [Tv + text_valid, T)."""
     B, H, T, D = q.shape
     scale = D ** -0.5 if scale is None else scale
     BH = B * H
     Tv = T - text_tokens
     assert 0 <= text_tokens < T
+    tval = text_tokens if text_valid is None else text_valid
+    assert 0 <= tval <= text_tokens
+    seg = Tv + tval
     q3, k3, v3 = (t.reshape(BH, T, D).to(dtype) for t in (q, k, v))
     if text_tokens:
         full = (q3, k3, v3)
@@ -301,15 +309,18 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
     out = torch.empty(BH, T, D, dtype=dtype)
     for b in range(BH):
         xk = xv = None
-        if text_tokens:
-            xk, xv = full[1][b, Tv:], full[2][b, Tv:]
+        if tval:
+            xk, xv = full[1][b, Tv:seg], full[2][b, Tv:seg]
         out[b, :Tv] = _attention_one(q3[b], k3[b], v3[b], st.kc[b], st.vc[b], hgroup[b], idx[b], st.n,
                                      block_size, group_size, scale, gamma, chunk, ref_precision, xk, xv)
-        if text_tokens:   # dense text rows, in the same base-2 arithmetic
-            x = (scale * LOG2E) * torch.matmul(full[0][b, Tv:], full[1][b].T)
+        # dense text rows, in the same base-2 arithmetic: each segment attends to itself
+        for r0, r1, k0, k1 in ((Tv, seg, 0, seg), (seg, T, seg, T)):
+            if r1 <= r0:
+                continue
+            x = (scale * LOG2E) * torch.matmul(full[0][b, r0:r1], full[1][b, k0:k1].T)
             p = torch.exp2(x - x.amax(-1, keepdim=True))
-            o = torch.matmul(p, full[2][b]) / p.sum(-1, keepdim=True)
-            out[b, Tv:] = _bf16(o) if ref_precision else o
+            o = torch.matmul(p, full[2][b, k0:k1]) / p.sum(-1, keepdim=True)
+            out[b, r0:r1] = _bf16(o) if ref_precision else o
     out = out.reshape(B, H, T, D)
     if return_aux:
         return out, dict(stats=st, hgroup=hgroup, scores=scores, idx=idx)
@@ -321,16 +332,19 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
 # ----------------------------------------------------------------------------
 
 def pisa_pg_attention_loop(q, k, v, idx, block_size: int, group_size: int, scale: float,
-                           gamma: str = "literal", dtype=torch.float64, text_tokens: int = 0):
+                           gamma: str = "literal", dtype=torch.float64, text_tokens: int = 0,
+                           text_valid: Optional[int] = None):
     """Literal restatement of pisa_pg_fwd_kernel's loops for one slice.
 
     q, k, v [T, D]; idx [NT, NS].  Phase 1 walks idx in order (:170-186); phase 2
     walks groups in order with the O(NS) selection re-test (:212-253); Gamma is
     rescaled only when gamma == 'consistent'.  Intended for tiny inputs.
     text_tokens: the last rows are text: phase 1 of each video row then walks the
-    text keys one by one; text rows run one online-softmax pass over every key."""
+    (valid) text keys one by one; text rows run one online-softmax pass over every key
+    of their segment (see pisa_pg_attention's text_valid)."""
     q, k, v = (t.to(dtype) for t in (q, k, v))
     T_all = q.shape[0]
+    tval = text_tokens if text_valid is None else text_valid
     if text_tokens:
         qt, kt, vt = q[-text_tokens:], k[-text_tokens:], v[-text_tokens:]
         kall, vall = k, v
@@ -360,7 +374,7 @@ def pisa_pg_attention_loop(q, k, v, idx, block_size: int, group_size: int, scale
                 l = l * alpha + p.sum()
                 acc = acc * alpha + sum(p[u] * v[t] for u, t in enumerate(ks))
                 m = new_m
-            for t in range(text_tokens):                   # text keys, exact
+            for t in range(tval):                          # valid text keys, exact
                 s_t = c * (qi @ kt[t])
                 new_m = torch.maximum(m, s_t)
                 alpha = torch.exp2(m - new_m)
@@ -399,7 +413,8 @@ def pisa_pg_attention_loop(q, k, v, idx, block_size: int, group_size: int, scale
             acc = torch.zeros(D, dtype=dtype)
             l = torch.tensor(0.0, dtype=dtype)
             m = torch.tensor(float("-inf"), dtype=dtype)
-            for t in range(T_all):
+            keys = range(0, T + tval) if i < tval else range(T + tval, T_all)
+            for t in keys:
                 s_t = c * (qt[i] @ kall[t])
                 new_m = torch.maximum(m, s_t)
                 alpha = torch.exp2(m - new_m)

@@ -55,14 +55,14 @@ SIGNATURES = {
     "pasa_select_workspace_bytes": (_sz, [_i64, _i64]),
     "pasa_select_from_scores": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp]),
     "pasa_sparse_attn": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
-                                _i64, _i64, _i64, _i64, _int, _int, _vp, _sz, _vp]),
+                                _i64, _i64, _i64, _i64, _i64, _int, _int, _vp, _sz, _vp]),
     "pasa_sparse_attn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "pasa_pack_phase2": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "pasa_sparse_attn_packed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
-                                       _i64, _i64, _i64, _i64, _int, _int, _vp]),
+                                       _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class PasaError(RuntimeError):

@@ -239,7 +239,9 @@ static int check_attn_shape(int64_t bh, int64_t seq_len, int64_t text_len, int64
   if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
   if ((rc = check_text(seq_len, text_len, head_dim))) return rc;
   if (group_size != 32) return fail(PASA_ERR_GROUP_SIZE, "group_size %lld != 32", (long long)group_size);
-  const int64_t grid = 8 * bh * cdiv(cdiv(seq_len - text_len, block_size), 8) + 8 * cdiv(bh * cdiv(text_len, block_size), 8);
+  // text query tiles: at most one more than cdiv(text_len, block_size) (prompt and padding split)
+  const int64_t grid = 8 * bh * cdiv(cdiv(seq_len - text_len, block_size), 8) +
+                       8 * cdiv(bh * (cdiv(text_len, block_size) + 1), 8);
   if (grid > kMaxI32) return fail(PASA_ERR_OVERFLOW, "grid too large");
   return PASA_OK;
 }
@@ -266,12 +268,15 @@ int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void
 
 static int check_attn_args(const void* q, const void* k, const void* v, const int32_t* idx,
                            const uint32_t* selmask, const void* o, double scale, int64_t bh,
-                           int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
-                           int64_t group_size, int64_t ns, int gamma_literal, int dtype) {
+                           int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim,
+                           int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype) {
   if (!q || !k || !v || !idx || !selmask || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
   if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_sparse_attn: only bf16 inputs are supported");
   int rc;
   if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
+  if (text_valid < 0 || text_valid > text_len)
+    return fail(PASA_ERR_TEXT_SEGMENT, "text_valid=%lld must be in [0, text_len=%lld]", (long long)text_valid,
+                (long long)text_len);
   const int64_t nt = cdiv(seq_len - text_len, block_size);
   if (ns < 1 || ns > nt) return fail(PASA_ERR_NUM_SELECTED, "ns=%lld not in [1, %lld]", (long long)ns, (long long)nt);
   if (nt > INT64_MAX / bh / ns) return fail(PASA_ERR_OVERFLOW, "bh*NT*ns overflows");
@@ -282,28 +287,30 @@ static int check_attn_args(const void* q, const void* k, const void* v, const in
 
 int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack, size_t pack_bytes,
                             const int32_t* idx, const uint32_t* selmask, void* o, double scale, int64_t bh,
-                            int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
-                            int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* stream) {
+                            int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim,
+                            int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype,
+                            void* stream) {
   int rc;
-  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, head_dim, block_size,
-                            group_size, ns, gamma_literal, dtype)))
+  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, text_valid, head_dim,
+                            block_size, group_size, ns, gamma_literal, dtype)))
     return rc;
   if ((rc = check_pack(pack, pack_bytes, bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
   return launch_status(pasa::launch_sparse_attn(q, k, v, pack, idx, selmask, o, (float)scale, (int)bh,
-                                                (int)(seq_len - text_len), (int)text_len, (int)head_dim,
-                                                (int)block_size, (int)ns, gamma_literal, (hipStream_t)stream),
+                                                (int)(seq_len - text_len), (int)text_len, (int)text_valid,
+                                                (int)head_dim, (int)block_size, (int)ns, gamma_literal,
+                                                (hipStream_t)stream),
                        "pasa_sparse_attn");
 }
 
 int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* kc, const float* vc,
                      const float* hgroup, const int32_t* idx, const uint32_t* selmask, void* o,
-                     double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
-                     int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype,
-                     void* workspace, size_t workspace_bytes, void* stream) {
+                     double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t text_valid,
+                     int64_t head_dim, int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal,
+                     int dtype, void* workspace, size_t workspace_bytes, void* stream) {
   if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
   int rc;
-  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, head_dim, block_size,
-                            group_size, ns, gamma_literal, dtype)))
+  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, text_valid, head_dim,
+                            block_size, group_size, ns, gamma_literal, dtype)))
     return rc;
   if ((rc = check_pack(workspace, workspace_bytes, bh, seq_len, text_len, head_dim, block_size, group_size)))
     return rc;
@@ -311,7 +318,8 @@ int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* k
                              block_size, group_size, stream)))
     return rc;
   return pasa_sparse_attn_packed(q, k, v, workspace, workspace_bytes, idx, selmask, o, scale, bh, seq_len,
-                                 text_len, head_dim, block_size, group_size, ns, gamma_literal, dtype, stream);
+                                 text_len, text_valid, head_dim, block_size, group_size, ns, gamma_literal,
+                                 dtype, stream);
 }
 
 }  // extern "C"

@@ -32,10 +32,11 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
                               int bh, int T, int D, int BT, hipStream_t stream);
 
 // T: rows of the blocked (video) segment; text: rows of the text segment that
-// follows it in each slice (slices are T + text rows apart).
+// follows it in each slice (slices are T + text rows apart), the first text_valid of
+// them the prompt and the rest padding.
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
-                              int bh, int T, int text, int D, int BT, int NS, int gamma_literal,
-                              hipStream_t stream);
+                              int bh, int T, int text, int text_valid, int D, int BT, int NS,
+                              int gamma_literal, hipStream_t stream);
 
 }  // namespace pasa

@@ -570,7 +570,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
                         const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
                         const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o,
                         float scale, float c, int T, int NT, int NG, int NW, int xcd_chunk,
-                        int gamma_literal, int text, int n_text_wg, int nbh) {
+                        int gamma_literal, int text, int text_valid, int n_text_wg, int nbh) {
   using C = K4D<BT>;
   using PK = typename C::PK;
   constexpr int D = 128;
@@ -578,21 +578,34 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   __shared__ __attribute__((aligned(1024))) unsigned char Ks[C::KBUF];
   __shared__ __attribute__((aligned(1024))) unsigned char Vs[C::VBUF];
 
-  // Each slice holds T blocked (video) rows followed by `text` text rows.  The first
-  // n_text_wg workgroups (a multiple of 8) each own one tile of text query rows and
-  // attend densely to every key; they are the longest-running ones, so they go first.
-  // The rest own one query block of the video rows; wg & 7 names their XCD, and each
-  // XCD takes a contiguous run of a slice's query blocks (shared K/V tiles in its L2).
+  // Each slice holds T blocked (video) rows followed by `text` text rows, of which the
+  // first text_valid are the prompt and the rest padding.  Two segments attend only
+  // within themselves: [0, seg) with seg = T + text_valid, and the padding [seg, T + text).
+  // The first n_text_wg workgroups (a multiple of 8) each own one tile of text query
+  // rows of one segment and attend densely to that segment's keys; they are the
+  // longest-running ones, so they go first.  The rest own one query block of the video
+  // rows; wg & 7 names their XCD, and each XCD takes a contiguous run of a slice's
+  // query blocks (shared K/V tiles in its L2).
   const int wg = blockIdx.x;
   const bool dense = wg < n_text_wg;
-  int bh, qb, qrow0, row_limit;
+  const int seg = T + text_valid;
+  int bh, qb, qrow0, row_limit, kbeg = 0, kend = seg;
   if (dense) {
-    const int qtiles = (text + BT - 1) / BT;
+    const int vtiles = (text_valid + BT - 1) / BT;
+    const int qtiles = vtiles + (text - text_valid + BT - 1) / BT;
     bh = wg / qtiles;
     if (bh >= nbh) return;  // padding of the text range to a multiple of 8
     qb = 0;
-    qrow0 = T + (wg - bh * qtiles) * BT;
-    row_limit = T + text;
+    const int qt = wg - bh * qtiles;
+    if (qt < vtiles) {
+      qrow0 = T + qt * BT;
+      row_limit = seg;
+    } else {
+      qrow0 = seg + (qt - vtiles) * BT;
+      row_limit = T + text;
+      kbeg = seg;
+      kend = T + text;
+    }
   } else {
     const int w = wg - n_text_wg;
     const int xcd = w & 7;
@@ -698,27 +711,24 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     return j;
   };
   // Exact tiles in visiting order: a video query block takes its selected blocks in
-  // ascending order, then the text rows; a text query tile takes every row of the slice.
-  // Returns the tile's first row (-1 when done) and its number of valid rows in nv.
+  // ascending order, then the prompt rows [T, seg); a text query tile takes every row
+  // of its segment [kbeg, kend).  Returns the tile's first row (-1 when done) and its
+  // number of valid rows in nv.
   int tt = 0;
-  const int text_tiles = (text + BT - 1) / BT;
-  const int all_tiles = (Ttot + BT - 1) / BT;
   auto next_tile = [&](int& nv) -> int {
-    if (dense) {
-      if (tt >= all_tiles) return -1;
-      const int r = tt++ * BT;
-      nv = min(BT, Ttot - r);
-      return r;
+    if (!dense) {
+      const int j = next_selected();
+      if (j >= 0) {
+        nv = min(BT, T - j * BT);
+        return j * BT;
+      }
+      kbeg = T;  // then the prompt rows
     }
-    const int j = next_selected();
-    if (j >= 0) {
-      nv = min(BT, T - j * BT);
-      return j * BT;
-    }
-    if (tt >= text_tiles) return -1;
-    const int r = tt++ * BT;
-    nv = min(BT, text - r);
-    return T + r;
+    const int r = kbeg + tt * BT;
+    if (r >= kend) return -1;
+    ++tt;
+    nv = min(BT, kend - r);
+    return r;
   };
 
   // ---------------- Phase 1 ------------------------------------------------------
@@ -1018,14 +1028,16 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
 
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
-                              int bh, int T, int text, int D, int BT, int NS, int gamma_literal,
-                              hipStream_t stream) {
+                              int bh, int T, int text, int text_valid, int D, int BT, int NS,
+                              int gamma_literal, hipStream_t stream) {
   if (text > 0 && D != 128) return hipErrorInvalidValue;  // the text segment is a D = 128 feature
+  if (text_valid < 0 || text_valid > text) return hipErrorInvalidValue;
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + kGroup - 1) / kGroup;
   const int NW = (NT + 31) / 32;
   const int xcd_chunk = (NT + 7) / 8;
-  const int n_text_wg = text > 0 ? (bh * ((text + BT - 1) / BT) + 7) / 8 * 8 : 0;
+  const int text_qtiles = (text_valid + BT - 1) / BT + (text - text_valid + BT - 1) / BT;
+  const int n_text_wg = (bh * text_qtiles + 7) / 8 * 8;
   dim3 grid(n_text_wg + 8 * bh * xcd_chunk);
   dim3 grid_video(8 * bh * xcd_chunk);
   const float c = scale * kLog2e;
@@ -1039,10 +1051,10 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
                      b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
   if (D == 128 && BT == 128)
     hipLaunchKernelGGL((k4_sparse_attn_dma<128>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, n_text_wg, bh);
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k4_sparse_attn_dma<64>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, n_text_wg, bh);
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
   else if (D == 64 && BT == 64)

@@ -151,8 +151,11 @@ def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_t
 
 def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: torch.Tensor,
                        sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
-                       out: Optional[torch.Tensor] = None, text_tokens: int = 0) -> torch.Tensor:
-    """K4 on operands from ``pack_phase2``."""
+                       out: Optional[torch.Tensor] = None, text_tokens: int = 0,
+                       text_valid: Optional[int] = None) -> torch.Tensor:
+    """K4 on operands from ``pack_phase2``.  ``text_valid`` (default: all
+    ``text_tokens``) is the number of prompt rows at the start of the text segment;
+    the rest are padding (see ``pisa_pg_attention``)."""
     _check_device(q, k, v, pack)
     if gamma not in ("literal", "consistent"):
         raise ValueError("gamma must be 'literal' or 'consistent'")
@@ -161,20 +164,22 @@ def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: 
     _check_device(o)
     _lib.call("pasa_sparse_attn_packed", q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(),
               pack.numel(), sel.idx.data_ptr(), sel.selmask.data_ptr(), o.data_ptr(), float(scale),
-              B * H, T, int(text_tokens), D, block_size, GROUP_SIZE, sel.ns, int(gamma == "literal"),
+              B * H, T, int(text_tokens), int(text_tokens if text_valid is None else text_valid), D,
+              block_size, GROUP_SIZE, sel.ns, int(gamma == "literal"),
               _DTYPES.get(q.dtype, -1), _stream(q))
     return o
 
 
 def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockStats,
                 sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
-                out: Optional[torch.Tensor] = None, text_tokens: int = 0) -> torch.Tensor:
+                out: Optional[torch.Tensor] = None, text_tokens: int = 0,
+                text_valid: Optional[int] = None) -> torch.Tensor:
     """Exact attention over the selected blocks plus the per-group first-order
     correction of the rest (reference pisa_pg_fwd_kernel :135-262); with
-    ``text_tokens``, the text keys are exact for every video query block and the
-    text rows are dense."""
+    ``text_tokens``, the prompt keys are exact for every video query block and the
+    text rows are dense within their segment."""
     pack = pack_phase2(q, stats, block_size, text_tokens)
-    return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out, text_tokens)
+    return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out, text_tokens, text_valid)
 
 
 def pisa_pg_attention(
@@ -192,6 +197,7 @@ def pisa_pg_attention(
     noise: Optional[torch.Tensor] = None,
     gamma: str = "literal",
     text_tokens: int = 0,
+    text_valid: Optional[int] = None,
 ):
     """PISA with per-group first-order correction (drop-in for reference :307-398).
 
@@ -206,7 +212,13 @@ def pisa_pg_attention(
     ``text_tokens``: the last rows are a text segment (HunyuanVideo's layout):
     blocks, selection and correction cover the video rows, every video query block
     attends to the text keys exactly and text rows attend densely to all keys.  The
-    default 0 is the reference's behaviour (text as ordinary tokens)."""
+    default 0 is the reference's behaviour (text as ordinary tokens).
+    ``text_valid``: only the first ``text_valid`` text rows are the prompt, the rest
+    padding (HunyuanVideo pads its prompt; its dense path attends block-diagonally
+    over cu_seqlens [0, T - text_tokens + text_valid, T], reference
+    svg/models/hyvideo/attention.py:314-322).  Video and prompt rows then see the
+    video rows and the prompt keys; padding rows see the padding keys.  Default:
+    ``text_tokens`` (no padding)."""
     B, H, T, D = q.shape
     if group_size != GROUP_SIZE:
         raise ValueError(f"the gfx950 kernels use group_size={GROUP_SIZE}")
@@ -219,4 +231,5 @@ def pisa_pg_attention(
     if verbose:
         print(f"NT={NT}, N_GROUPS={stats.hgroup.shape[2]}, GROUP_SIZE={group_size}")
         print(f"top_k={sel.ns}, density={density}")
-    return sparse_attn(q, k, v, stats, sel, scale, block_size, gamma, text_tokens=text_tokens)
+    return sparse_attn(q, k, v, stats, sel, scale, block_size, gamma, text_tokens=text_tokens,
+                       text_valid=text_valid)

@@ -24,7 +24,9 @@ Notes on the reference:
 * The sparse call passes the whole joint sequence, text tokens included, to
   ``pisa_pg_attention`` with block_size=64 (:680): text tokens are ordinary tokens.
   ``text_segment = True`` (class attribute) instead treats the trailing
-  ``context_length`` tokens as a text segment (``pisa_pg_attention(text_tokens=...)``).
+  ``context_length`` tokens as a text segment (``pisa_pg_attention(text_tokens=...)``)
+  and honours the attention mask there as the dense path does: the text tokens past
+  the mask's valid prefix are padding (``text_valid=...``), a segment of their own.
 Left out (not on the hot path): sample_mse / flex-attention SVG masks (:382-411).
 """
 from __future__ import annotations
@@ -257,8 +259,9 @@ class Hunyuan_PASA_Processor(Hunyuan_SVGAttn_Processor2_0):
     block_size = 64        # the reference's call site passes block_size=64 (:680)
     logging_file = None
     # False (the reference): the text tokens are ordinary tokens of the sparse call.
-    # True: the last context_length tokens are a text segment (exact text keys for
-    # every video query block, dense text rows); needs head_dim 128.
+    # True: the last context_length tokens are a text segment (exact prompt keys for
+    # every video query block, dense text rows, the mask's padding a segment of its
+    # own as in the dense path); needs head_dim 128.
     text_segment = False
 
     def __init__(self, layer_idx):
@@ -287,7 +290,11 @@ class Hunyuan_PASA_Processor(Hunyuan_SVGAttn_Processor2_0):
         if not self.use_group:
             raise NotImplementedError("use_group=False selects piecewise_sparse_attention "
                                       "(svg/kernels/triton/pisa_attention.py), which this build does not provide")
-        extra = {"text_tokens": context_length} if self.text_segment else {}
+        extra = {}
+        if self.text_segment:
+            video = seq_len - context_length
+            valid = int(cu_max_seqlens[0][1])   # cu_seqlens [0, valid, N]
+            extra = {"text_tokens": context_length, "text_valid": min(max(valid - video, 0), context_length)}
         out = pisa_pg_attention(query.contiguous(), key.contiguous(), value.contiguous(), density=density,
                                 block_size=self.block_size, use_random=self.use_random, **extra)
         return out.reshape(cfg, num_heads, seq_len, dim)

@@ -142,10 +142,11 @@ def test_select_from_scores_validation(lib):
 
 def attn(lib, **kw):
     a = dict(q=FAKE, k=FAKE, v=FAKE, kc=FAKE, vc=FAKE, hg=FAKE, idx=FAKE, mask=FAKE, o=FAKE, scale=0.1,
-             bh=2, T=1000, text=0, D=128, BT=128, G=32, ns=2, lit=1, dtype=0, ws=FAKE, wsb=1 << 30)
+             bh=2, T=1000, text=0, tv=None, D=128, BT=128, G=32, ns=2, lit=1, dtype=0, ws=FAKE, wsb=1 << 30)
     a.update(kw)
+    tv = a["text"] if a["tv"] is None else a["tv"]
     return lib.pasa_sparse_attn(a["q"], a["k"], a["v"], a["kc"], a["vc"], a["hg"], a["idx"], a["mask"],
-                                a["o"], a["scale"], a["bh"], a["T"], a["text"], a["D"], a["BT"], a["G"],
+                                a["o"], a["scale"], a["bh"], a["T"], a["text"], tv, a["D"], a["BT"], a["G"],
                                 a["ns"], a["lit"], a["dtype"], a["ws"], a["wsb"], None)
 
 
@@ -155,7 +156,8 @@ def attn(lib, **kw):
     (dict(scale=0.0), -9), (dict(scale=-1.0), -9), (dict(scale=float("nan")), -9),
     (dict(lit=2), -9), (dict(ws=None), -8), (dict(wsb=10), -8), (dict(T=0), -2),
     (dict(T=(1 << 24) - 100), -6), (dict(text=1000), -10), (dict(text=-3), -10),
-    (dict(text=100, D=64), -10), (dict(text=200, ns=8), -5),
+    (dict(text=100, D=64), -10), (dict(text=200, ns=8), -5), (dict(text=100, tv=101), -10),
+    (dict(text=100, tv=-1), -10), (dict(text=0, tv=1), -10),
 ])
 def test_sparse_attn_validation(lib, kw, code):
     assert attn(lib, **kw) == code
@@ -170,14 +172,16 @@ def test_packed_entry_validation(lib):
     assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 16, None) == -12
     assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 1000, 128, 128, 32, None) == -10
     f = lib.pasa_sparse_attn_packed
-    args = [FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, 2, 1000, 0, 128, 128, 32, 2, 1, 0, None]
+    args = [FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, 2, 1000, 0, 0, 128, 128, 32, 2, 1, 0, None]
     bad = list(args); bad[4] = 0
     assert f(*bad) == -8
-    bad = list(args); bad[15] = 100
+    bad = list(args); bad[16] = 100
     assert f(*bad) == -5
-    bad = list(args); bad[17] = 2
+    bad = list(args); bad[18] = 2
     assert f(*bad) == -7
     bad = list(args); bad[11] = -1
+    assert f(*bad) == -10
+    bad = list(args); bad[12] = 1     # text_valid > text_len
     assert f(*bad) == -10
 
 

@@ -297,10 +297,15 @@ def test_end_to_end_c2_full_shape(device):
 # ------------------------------------------------------------ text segment --
 
 TEXT_CASES = [
-    # heads, grid, text, BT, density, gamma
-    (2, (3, 10, 20), 40, 128, 0.4, "literal"),      # last video block 88 rows; one partial text tile
-    (1, (5, 13, 17), 256, 64, 0.2, "literal"),      # BT 64 kernel; four text tiles
-    (2, (3, 10, 20), 300, 128, 0.3, "consistent"),  # three text tiles, the last partial
+    # heads, grid, text, BT, density, gamma, prompt rows (None: no padding)
+    (2, (3, 10, 20), 40, 128, 0.4, "literal", None),      # last video block 88 rows; one partial text tile
+    (1, (5, 13, 17), 256, 64, 0.2, "literal", None),      # BT 64 kernel; four text tiles
+    (2, (3, 10, 20), 300, 128, 0.3, "consistent", None),  # three text tiles, the last partial
+    (2, (3, 10, 20), 300, 128, 0.3, "literal", 77),       # prompt 1 partial tile, padding 2 tiles
+    (2, (3, 10, 20), 256, 128, 0.4, "literal", 128),      # segment edge on a tile edge
+    (1, (5, 13, 17), 256, 64, 0.2, "consistent", 200),    # BT 64: 4 prompt tiles, 1 padding tile
+    (1, (5, 13, 17), 256, 64, 0.2, "literal", 0),         # all padding: video rows see no text
+    (2, (3, 10, 20), 40, 128, 0.4, "literal", 39),        # one padding row
 ]
 
 
@@ -310,11 +315,11 @@ def text_inputs(heads, grid, text, BT, density, seed):
     return wl, make_inputs(wl, seed=seed, dtype=torch.bfloat16)
 
 
-@pytest.mark.parametrize("heads,grid,text,BT,density,gamma", TEXT_CASES)
-def test_text_segment_shared_selection(device, heads, grid, text, BT, density, gamma):
+@pytest.mark.parametrize("heads,grid,text,BT,density,gamma,valid", TEXT_CASES)
+def test_text_segment_shared_selection(device, heads, grid, text, BT, density, gamma, valid):
     wl, (q, k, v) = text_inputs(heads, grid, text, BT, density, seed=4)
     T, Tv = wl.seq_len, wl.video_tokens
-    say(f"[text] heads={heads} Tv={Tv} text={text} BT={BT} density={density} gamma={gamma}")
+    say(f"[text] heads={heads} Tv={Tv} text={text} valid={valid} BT={BT} density={density} gamma={gamma}")
     qd, kd, vd = q.to(device), k.to(device), v.to(device)
     scale = 128 ** -0.5
     st = ops.block_stats(qd, kd, vd, BT, 32, text_tokens=text)
@@ -323,14 +328,18 @@ def test_text_segment_shared_selection(device, heads, grid, text, BT, density, g
     torch.testing.assert_close(st.kc[0].cpu().double(), ref_st.kc, rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(st.vc[0].cpu().double(), ref_st.vc, rtol=1e-5, atol=1e-4)
     sel = ops.select_blocks(st, density, scale)
-    o = ops.sparse_attn(qd, kd, vd, st, sel, scale, BT, gamma, text_tokens=text)
+    o = ops.sparse_attn(qd, kd, vd, st, sel, scale, BT, gamma, text_tokens=text, text_valid=valid)
     idx = sel.idx.cpu()
-    ref = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, gamma=gamma, indices=idx, text_tokens=text)
-    rp = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, gamma=gamma, indices=idx, text_tokens=text,
-                             ref_precision=True)
+    kw = dict(gamma=gamma, indices=idx, text_tokens=text, text_valid=valid)
+    ref = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, **kw)
+    rp = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, ref_precision=True, **kw)
     floor = O.parity_metrics(rp, ref)
-    check_parity(o.cpu(), ref, f"text {Tv}+{text} BT{BT} {gamma}", floor)
-    check_parity(o.cpu()[..., Tv:, :], ref[..., Tv:, :], "text rows (dense)")
+    check_parity(o.cpu(), ref, f"text {Tv}+{text} valid {valid} BT{BT} {gamma}", floor)
+    seg = Tv + (text if valid is None else valid)
+    if seg > Tv:
+        check_parity(o.cpu()[..., Tv:seg, :], ref[..., Tv:seg, :], "prompt rows (dense)")
+    if seg < T:
+        check_parity(o.cpu()[..., seg:, :], ref[..., seg:, :], "padding rows (dense)")
 
 
 def test_text_segment_full_density_equals_dense_attention(device):
@@ -340,6 +349,21 @@ def test_text_segment_full_density_equals_dense_attention(device):
                               text_tokens=100)
     ref = O.dense_attention(q.double(), k.double(), v.double(), O.effective_scale(128 ** -0.5))
     check_parity(o.cpu(), ref, "text density=1")
+
+
+def test_text_padding_full_density_is_block_diagonal(device):
+    # cu_seqlens [0, seg, T] semantics: two independent dense attentions
+    wl, (q, k, v) = text_inputs(2, (3, 10, 20), 100, 128, 1.0, seed=6)
+    seg = wl.video_tokens + 37
+    say(f"[text] density 1.0, 37 of 100 text rows valid vs two dense attentions (split at {seg})")
+    o = ops.pisa_pg_attention(q.to(device), k.to(device), v.to(device), density=1.0, block_size=128,
+                              text_tokens=100, text_valid=37).cpu()
+    es = O.effective_scale(128 ** -0.5)
+    qd, kd, vd = q.double(), k.double(), v.double()
+    check_parity(o[..., :seg, :], O.dense_attention(qd[..., :seg, :], kd[..., :seg, :], vd[..., :seg, :], es),
+                 "segment [0, seg)")
+    check_parity(o[..., seg:, :], O.dense_attention(qd[..., seg:, :], kd[..., seg:, :], vd[..., seg:, :], es),
+                 "padding segment")
 
 
 def test_end_to_end_c3_one_head_text_segment(device):

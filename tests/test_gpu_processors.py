@@ -89,3 +89,42 @@ def test_wan_pasa_processor_sparse_call(device, monkeypatch):
     finally:
         for a, val in saved.items():
             setattr(M, a, val)
+
+
+def test_hunyuan_pasa_processor_text_segment_with_padding(device, monkeypatch):
+    # text_segment: the mask's padding is a segment of its own, as in the dense path
+    torch.manual_seed(2)
+    M = HY.Hunyuan_PASA_Processor
+    saved = {a: getattr(M, a) for a in ("context_length", "num_frame", "frame_size", "first_layers_fp",
+                                        "first_times_fp", "rescaled_density", "use_random", "text_segment")}
+    try:
+        M.context_length, M.num_frame, M.frame_size = 40, 4, 60       # 240 video + 40 text tokens
+        M.first_layers_fp, M.first_times_fp = 0, 900
+        M.rescaled_density, M.use_random, M.text_segment = {500: 0.5}, False, True
+        spy = Spy(HY.pisa_pg_attention)
+        monkeypatch.setattr(HY, "pisa_pg_attention", spy)
+        C, H = 256, 2
+        attn = MockAttn(C, H, joint_text=True).to(device, torch.bfloat16)
+        x = torch.randn(1, 240, C, device=device, dtype=torch.bfloat16)
+        enc = torch.randn(1, 40, C, device=device, dtype=torch.bfloat16)
+        mask = torch.zeros(1, 1, 1, 280, dtype=torch.bool, device=device)
+        mask[..., :240 + 23] = True                                    # 23 prompt tokens, 17 padding
+        cos, sin = rope_tables(240, C // H)
+        with torch.no_grad():
+            M(3)(attn, x, enc, mask, (cos.to(device), sin.to(device)), timestep=torch.tensor([500]))
+        torch.cuda.synchronize()
+        assert len(spy.calls) == 1
+        q, k, v, o, kw = spy.calls[0]
+        assert kw["text_tokens"] == 40 and kw["text_valid"] == 23
+        scale = q.shape[-1] ** -0.5
+        st = ops.block_stats(q, k, v, 64, 32, text_tokens=40)
+        sel = ops.select_blocks(st, 0.5, scale)
+        ref = O.pisa_pg_attention(q.cpu().float(), k.cpu().float(), v.cpu().float(), 0.5, 64, 32, scale,
+                                  indices=sel.idx.cpu(), text_tokens=40, text_valid=23)
+        m = O.parity_metrics(o.cpu().float(), ref)
+        print(f"[proc] hunyuan text segment 23/40 cos={m['cos']:.7f} excess/rms={m['excess_over_rms']:.3e}",
+              flush=True)
+        assert m["bound_ok"], m
+    finally:
+        for a, val in saved.items():
+            setattr(M, a, val)

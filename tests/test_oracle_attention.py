@@ -219,3 +219,36 @@ def test_text_segment_with_negligible_text_keys_is_video_only_pisa():
     out = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, s, dtype=f64, text_tokens=16)
     ref = O.pisa_pg_attention(q[..., :80, :], k[..., :80, :], v[..., :80, :], 0.25, 16, 2, s, dtype=f64)
     torch.testing.assert_close(out[..., :80, :], ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("text,valid", [(12, 5), (17, 0), (20, 20), (33, 30)])
+def test_text_padding_closed_form_matches_sequential_loop(text, valid):
+    T = 96 + text
+    q, k, v = rand_qkv(1, 2, T, 6, seed=text + valid, scale=1.5)
+    s = 6 ** -0.5
+    out, aux = O.pisa_pg_attention(q, k, v, 0.3, 16, 2, s, dtype=f64, return_aux=True, text_tokens=text,
+                                   text_valid=valid)
+    for b in range(2):
+        ref = O.pisa_pg_attention_loop(q[0, b], k[0, b], v[0, b], aux["idx"][b], 16, 2, s, text_tokens=text,
+                                       text_valid=valid)
+        torch.testing.assert_close(out[0, b], ref, rtol=1e-10, atol=1e-10)
+
+
+def test_text_padding_is_block_diagonal_for_text_rows():
+    # Text rows reduce to dense attention within their segment; video rows ignore padding keys.
+    q, k, v = rand_qkv(1, 1, 110, 8, seed=9)
+    s = 8 ** -0.5
+    Tv, seg = 80, 92
+    out = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, s, dtype=f64, text_tokens=30, text_valid=12)
+    es = O.effective_scale(s)
+    torch.testing.assert_close(out[..., Tv:seg, :], O.dense_attention(q[..., Tv:seg, :], k[..., :seg, :],
+                                                                     v[..., :seg, :], es), rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(out[..., seg:, :], O.dense_attention(q[..., seg:, :], k[..., seg:, :],
+                                                                   v[..., seg:, :], es), rtol=1e-10, atol=1e-10)
+    k2, v2 = k.clone(), v.clone()
+    k2[..., seg:, :] = torch.randn(18, 8, dtype=f64)   # padding keys/values do not reach video rows
+    v2[..., seg:, :] = torch.randn(18, 8, dtype=f64)
+    out2 = O.pisa_pg_attention(q, k2, v2, 0.25, 16, 2, s, dtype=f64, text_tokens=30, text_valid=12)
+    torch.testing.assert_close(out2[..., :seg, :], out[..., :seg, :], rtol=0, atol=0)
+    full = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, s, dtype=f64, text_tokens=30)
+    assert not torch.allclose(full[..., :Tv, :], out[..., :Tv, :])   # padding keys matter when unmasked

@@ -226,10 +226,14 @@ def test_hunyuan_pasa_dispatch(monkeypatch, hy_config):
     hy_config.text_segment = True
     try:
         hy_config(5).attention_core_logic(q, q, q, torch.tensor([500]), 5, cu)
+        assert rec.calls[-1] == dict(density=0.2 * 0.9239564591192239, block_size=64, use_random=True,
+                                     text_tokens=3, text_valid=3)
+        # mask valid prefix 9 of 11: 8 video tokens + 1 prompt token, 2 padding
+        cu9 = (torch.tensor([0, 9, 11]), torch.tensor([0, 9, 11]), 9, 9)
+        hy_config(5).attention_core_logic(q, q, q, torch.tensor([500]), 5, cu9)
+        assert rec.calls[-1]["text_tokens"] == 3 and rec.calls[-1]["text_valid"] == 1
     finally:
         hy_config.text_segment = False
-    assert rec.calls[-1] == dict(density=0.2 * 0.9239564591192239, block_size=64, use_random=True,
-                                 text_tokens=3)
 
 
 def test_hunyuan_pasa_use_group_false_raises(monkeypatch, hy_config):
