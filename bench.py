@@ -51,7 +51,7 @@ def main() -> int:
         return 2
 
     import torch
-    from pasa_amd import _lib, ops, placement
+    from pasa_amd import _lib, ops, placement, prologue
     from pasa_amd.workloads import WORKLOADS, make_inputs
 
     wl = WORKLOADS[args.workload]
@@ -136,6 +136,28 @@ def main() -> int:
     k2_bytes = 3 * tensor_bytes + H * NT * (3 * D + 1) * 4 + H * math.ceil(NT / 32) * D * D * 4
     log(f"K1 fwd {k1f:.3f} ms ({k1f_gbps:.0f} GB/s)  inv {k1i:.3f} ms ({k1i_gbps:.0f} GB/s)")
 
+    # K5: the Wan processor prologue at this shape: projections [1, T, H*D] -> RMSNorm over
+    # H*D (one rounding), head split, complex fp64 RoPE of Q and K; V moved.  Synthetic
+    # projections reuse Q/K/V's bytes; the outputs go to K1's buffers.
+    xs = [t.view(1, T, H * D) for t in (q, k, v)]
+    wts = [(torch.rand(H * D, device=q.device) + 0.5).to(torch.bfloat16) for _ in range(2)]
+    ang = torch.rand(T, D // 2, device=q.device, dtype=torch.float64) * 6.0
+    re_, im_ = torch.cos(ang), torch.sin(ang)
+    k5_args = dict(wq=wts[0], wk=wts[1], norm="row", rounding="once", eps=1e-6, rope=("complex", re_, im_),
+                   out=bufs)
+    for _ in range(3):
+        prologue.qkv_prologue(*xs, H, **k5_args)
+    ka.record()
+    for _ in range(reps):
+        prologue.qkv_prologue(*xs, H, **k5_args)
+    kb.record()
+    torch.cuda.synchronize()
+    k5 = ka.elapsed_time(kb) / reps
+    k5_bytes = 6 * tensor_bytes + 2 * T * (D // 2) * 8 + 2 * H * D * 2
+    k5_gbps = k5_bytes / (k5 * 1e-3) / 1e9
+    log(f"K5 prologue {k5:.3f} ms ({k5_gbps:.0f} GB/s algorithmic, {k5_bytes / 1e9:.2f} GB)")
+    del xs, wts, ang, re_, im_
+
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
@@ -207,6 +229,9 @@ def main() -> int:
                        "inv_ms": round(k1i, 4), "inv_GBps": round(k1i_gbps, 1),
                        "frac_of_hbm_peak_fwd": round(k1f_gbps / PEAK_HBM_GBPS, 4)},
         "k2_GBps_algorithmic": round(k2_bytes / (k2 * 1e-3) / 1e9, 1),
+        "k5_prologue": {"ms": round(k5, 4), "GBps": round(k5_gbps, 1), "bytes": k5_bytes,
+                        "frac_of_hbm_peak": round(k5_gbps / PEAK_HBM_GBPS, 4),
+                        "mode": "Wan: RMSNorm over H*D (one rounding) + head split + complex fp64 RoPE, Q/K/V"},
         "parity_vs_oracle": parity,
     }
     print(json.dumps(res), flush=True)

@@ -188,6 +188,62 @@ int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const v
                             int64_t text_valid, int64_t head_dim, int64_t block_size,
                             int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* stream);
 
+/* ---- Processor prologue (K5) ------------------------------------------------ */
+
+typedef enum {
+  PASA_LAYOUT_BHSD = 0,  /* [B, H, S, D]: head-major, what the attention entry points read */
+  PASA_LAYOUT_BSHD = 1   /* [B, S, H*D]: token-major, what the projections produce        */
+} pasa_layout_t;
+
+typedef enum {
+  PASA_NORM_NONE = 0,
+  PASA_NORM_HEAD = 1,    /* RMSNorm over each head's D channels; weight [D]      */
+  PASA_NORM_ROW = 2      /* RMSNorm over the token's H*D channels; weight [H*D]  */
+} pasa_norm_t;
+
+typedef enum {
+  PASA_NORM_ROUND_ONCE = 0,  /* y = bf16((x*rstd)*w), rstd = 1/sqrt(mean(x^2)+eps)          */
+  PASA_NORM_ROUND_TWICE = 1  /* y = bf16(bf16(x*rsqrt(mean(x^2)+eps))*w): diffusers RMSNorm */
+} pasa_norm_rounding_t;
+
+typedef enum {
+  PASA_ROPE_NONE = 0,
+  PASA_ROPE_COSSIN_F32 = 1,  /* cos, sin fp32 [rope_rows, D]; pairs (x[2i], x[2i+1]):
+                                o[2i] = x[2i]cos[2i] - x[2i+1]sin[2i],
+                                o[2i+1] = x[2i+1]cos[2i+1] + x[2i]sin[2i+1], fp32 steps */
+  PASA_ROPE_COMPLEX_F64 = 2  /* cos = Re, sin = Im, fp64 [rope_rows, D/2]; (x[2i] + i x[2i+1])
+                                times the coefficient in fp64, cast fp64 -> fp32 -> bf16     */
+} pasa_rope_t;
+
+/* Q/K RMSNorm and rotary embedding, fused with the head split, in one pass.
+ * xq, xk, xv: bf16 inputs in in_layout with `seq_len` rows per (b, h) (any may be
+ * NULL: that tensor is skipped; its output must then be NULL too).  q, k, v: bf16
+ * outputs in out_layout with out_seq_len rows per (b, h); input row s lands at
+ * output row out_row0 + s (so two calls can fill the video and text parts of one
+ * joint sequence).  wq, wk: bf16 RMSNorm weights ([D] for PASA_NORM_HEAD, [H*D]
+ * for PASA_NORM_ROW); a NULL weight leaves that tensor unnormalised.  V is only
+ * moved.  Rows s < rope_rows of Q and K are rotated after the norm; rows past it
+ * (trailing text tokens) are not.  Each step rounds to bf16 where the step-by-step
+ * reference does, so the result equals the unfused pipeline up to the order of
+ * the sum of squares.  Input and output may be the same buffer when in_layout ==
+ * out_layout, out_seq_len == seq_len and out_row0 == 0 (in place); other
+ * overlaps are not allowed.  head_dim 64 or 128; heads*head_dim <= 8192.
+ * Replaces: triton_rmsnorm_forward (svg/kernels/triton/rmsnorm.py:8-101) and the
+ * head split + rotary steps of the Wan processor (svg/models/wan/attention.py:31-57,
+ * :114-150, :182-188); the absent _kernels.rms_norm_forward and
+ * _kernels.apply_qk_rope_inplace_cossin_{txtlast,complex} (call sites
+ * svg/models/hyvideo/attention.py:162-190, svg/models/wan/attention.py:36-39), with
+ * the PyTorch fallbacks at hyvideo/attention.py:196-230 as their observable
+ * behaviour. */
+int pasa_qkv_prologue(const void* xq, const void* xk, const void* xv,
+                      void* q, void* k, void* v,
+                      const void* wq, const void* wk,
+                      int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim,
+                      int in_layout, int out_layout, int64_t out_seq_len, int64_t out_row0,
+                      int norm, int norm_rounding, double eps,
+                      const void* rope_cos, const void* rope_sin, int rope, int64_t rope_rows,
+                      int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -322,4 +322,77 @@ int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* k
                                  dtype, stream);
 }
 
+int pasa_qkv_prologue(const void* xq, const void* xk, const void* xv, void* q, void* k, void* v,
+                      const void* wq, const void* wk, int64_t batch, int64_t seq_len, int64_t heads,
+                      int64_t head_dim, int in_layout, int out_layout, int64_t out_seq_len, int64_t out_row0,
+                      int norm, int norm_rounding, double eps, const void* rope_cos, const void* rope_sin,
+                      int rope, int64_t rope_rows, int dtype, void* stream) {
+  const void* ins[3] = {xq, xk, xv};
+  void* outs[3] = {q, k, v};
+  bool any = false;
+  for (int t = 0; t < 3; ++t) {
+    if ((ins[t] == nullptr) != (outs[t] == nullptr))
+      return fail(PASA_ERR_NULL_POINTER, "pasa_qkv_prologue: tensor %d has only one of input/output", t);
+    any = any || ins[t] != nullptr;
+  }
+  if (!any) return fail(PASA_ERR_NULL_POINTER, "pasa_qkv_prologue: no tensor given");
+  if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_qkv_prologue: only bf16 is supported");
+  int rc;
+  if ((rc = check_head_dim(head_dim))) return rc;
+  if (batch <= 0 || seq_len <= 0 || heads <= 0 || out_seq_len <= 0)
+    return fail(PASA_ERR_BAD_SHAPE, "batch, seq_len, heads and out_seq_len must be > 0");
+  if (batch > 65535) return fail(PASA_ERR_BAD_SHAPE, "batch %lld > 65535", (long long)batch);
+  if (heads * (head_dim / 8) > pasa::prologue_max_chunks())
+    return fail(PASA_ERR_BAD_SHAPE, "heads*head_dim=%lld exceeds %d", (long long)(heads * head_dim),
+                pasa::prologue_max_chunks() * 8);
+  if (out_row0 < 0 || out_row0 > out_seq_len - seq_len)
+    return fail(PASA_ERR_BAD_SHAPE, "rows [%lld, %lld) do not fit out_seq_len=%lld", (long long)out_row0,
+                (long long)(out_row0 + seq_len), (long long)out_seq_len);
+  if (seq_len > INT64_MAX / batch / heads / head_dim || out_seq_len > INT64_MAX / batch / heads / head_dim ||
+      (seq_len + 3) / 4 > kMaxI32)
+    return fail(PASA_ERR_OVERFLOW, "pasa_qkv_prologue: sizes overflow");
+  if ((in_layout != PASA_LAYOUT_BHSD && in_layout != PASA_LAYOUT_BSHD) ||
+      (out_layout != PASA_LAYOUT_BHSD && out_layout != PASA_LAYOUT_BSHD))
+    return fail(PASA_ERR_BAD_ARG, "unknown layout");
+  if (norm != PASA_NORM_NONE && norm != PASA_NORM_HEAD && norm != PASA_NORM_ROW)
+    return fail(PASA_ERR_BAD_ARG, "unknown norm %d", norm);
+  if (norm_rounding != PASA_NORM_ROUND_ONCE && norm_rounding != PASA_NORM_ROUND_TWICE)
+    return fail(PASA_ERR_BAD_ARG, "unknown norm_rounding %d", norm_rounding);
+  if (!std::isfinite(eps) || eps < 0.0) return fail(PASA_ERR_BAD_ARG, "eps must be finite and >= 0");
+  if (norm != PASA_NORM_NONE && !wq && !wk)
+    return fail(PASA_ERR_NULL_POINTER, "a norm needs at least one of wq, wk");
+  if (rope != PASA_ROPE_NONE && rope != PASA_ROPE_COSSIN_F32 && rope != PASA_ROPE_COMPLEX_F64)
+    return fail(PASA_ERR_BAD_ARG, "unknown rope %d", rope);
+  if (rope != PASA_ROPE_NONE && (!rope_cos || !rope_sin))
+    return fail(PASA_ERR_NULL_POINTER, "rope tables are NULL");
+  if (rope != PASA_ROPE_NONE && (rope_rows < 0 || rope_rows > seq_len))
+    return fail(PASA_ERR_BAD_SHAPE, "rope_rows=%lld not in [0, seq_len=%lld]", (long long)rope_rows,
+                (long long)seq_len);
+  for (int t = 0; t < 3; ++t)
+    if (ins[t] && ins[t] == outs[t] && (in_layout != out_layout || out_seq_len != seq_len || out_row0 != 0))
+      return fail(PASA_ERR_BAD_ARG, "in place (tensor %d) needs equal layouts, out_seq_len == seq_len and "
+                  "out_row0 == 0", t);
+  pasa::PrologueParams p{};
+  const void* ws[3] = {wq, wk, nullptr};
+  for (int t = 0; t < 3; ++t)
+    p.t[t] = pasa::PrologueTensor{(const uint16_t*)ins[t], (uint16_t*)outs[t],
+                                  norm != PASA_NORM_NONE ? (const uint16_t*)ws[t] : nullptr};
+  p.cos = rope_cos;
+  p.sin = rope_sin;
+  p.B = batch;
+  p.S = seq_len;
+  p.H = heads;
+  p.OS = out_seq_len;
+  p.row0 = out_row0;
+  p.rope_rows = rope != PASA_ROPE_NONE ? rope_rows : 0;
+  p.D = (int)head_dim;
+  p.in_bshd = in_layout == PASA_LAYOUT_BSHD;
+  p.out_bshd = out_layout == PASA_LAYOUT_BSHD;
+  p.norm = norm == PASA_NORM_HEAD ? pasa::kNormHead : (norm == PASA_NORM_ROW ? pasa::kNormRow : 0);
+  p.round_twice = norm_rounding == PASA_NORM_ROUND_TWICE;
+  p.rope = rope == PASA_ROPE_COSSIN_F32 ? pasa::kRopeCosSinF32 : (rope == PASA_ROPE_COMPLEX_F64 ? pasa::kRopeComplexF64 : 0);
+  p.eps = (float)eps;
+  return launch_status(pasa::launch_prologue(p, (hipStream_t)stream), "pasa_qkv_prologue");
+}
+
 }  // extern "C"

@@ -39,4 +39,34 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
                               int bh, int T, int text, int text_valid, int D, int BT, int NS,
                               int gamma_literal, hipStream_t stream);
 
+// ---- K5: processor prologue (RMSNorm + rotary embedding + head-major layout) ----
+constexpr int kNormHead = 1;       // RMSNorm over each head's D channels, weight [D]
+constexpr int kNormRow = 2;        // RMSNorm over the token's H*D channels, weight [H*D]
+constexpr int kRopeCosSinF32 = 1;  // cos, sin: fp32 [rope_rows, D]
+constexpr int kRopeComplexF64 = 2; // cos = real, sin = imaginary part: fp64 [rope_rows, D/2]
+
+struct PrologueTensor {
+  const uint16_t* in;      // bf16; nullptr: tensor skipped
+  uint16_t* out;           // bf16
+  const uint16_t* weight;  // bf16 RMSNorm weight; nullptr: no norm for this tensor
+};
+
+struct PrologueParams {
+  PrologueTensor t[3];      // q, k (normalised and rotated), v (layout only)
+  const void* cos;
+  const void* sin;
+  int64_t B, S, H;          // batch, rows per (b, h) slice read, heads
+  int64_t OS, row0;         // output rows per slice and first output row
+  int64_t rope_rows;        // rows [0, rope_rows) are rotated
+  int D;
+  int in_bshd, out_bshd;    // 1: [B, S, H, D]; 0: [B, H, S, D]
+  int norm;                 // 0, kNormHead or kNormRow
+  int round_twice;          // 1: diffusers RMSNorm rounding; 0: one rounding
+  int rope;                 // 0, kRopeCosSinF32 or kRopeComplexF64
+  float eps;
+};
+
+int prologue_max_chunks();  // H * D / 8 limit
+hipError_t launch_prologue(const PrologueParams& p, hipStream_t stream);
+
 }  // namespace pasa

@@ -40,6 +40,8 @@ import torch.nn.functional as F
 from .. import density as _density
 from ..ops import pisa_pg_attention
 from ..placement import hunyuan_hidden_states_placement, hunyuan_sparse_head_placement
+from ..prologue import qkv_prologue, rope_tables_cossin
+from .qknorm import fusable, module_rounding, norm_eps
 from .rope import apply_rotary_emb_cos_sin
 from .timestep_hook import current_timestep, install_hunyuan
 
@@ -67,6 +69,64 @@ def _valid_length(attention_mask, n: int) -> int:
     return int(attention_mask.sum().item())
 
 
+def fused_hunyuan_qkv(attn, hidden_states, encoder_hidden_states, image_rotary_emb):
+    """Projections, per-head QK-norm, RoPE (video rows) and the text concat of the
+    HunyuanVideo processors (reference :52-100, :248-300) with the fused prologue
+    kernel: one pass per stream, written straight into the joint [B, H, N, D]
+    tensors.  Returns None when the inputs are outside what the kernel reproduces."""
+    H = attn.heads
+    C = hidden_states.shape[-1]
+    if C % H:
+        return None
+    D = C // H
+    joint = attn.add_q_proj is not None and encoder_hidden_states is not None
+    dt = hidden_states.dtype
+
+    def norm_args(mq, mk):
+        """(norm, rounding, eps) of one kernel call, or None if the pair is not reproducible."""
+        present = [m for m in (mq, mk) if m is not None]
+        if not present:
+            return None, "once", 0.0
+        rnd = {module_rounding(m) for m in present}
+        eps = {norm_eps(m, dt) for m in present}
+        if None in rnd or len(rnd) > 1 or len(eps) > 1:
+            return None
+        return "head", rnd.pop(), eps.pop()
+
+    video = norm_args(attn.norm_q, attn.norm_k)
+    text = norm_args(attn.norm_added_q, attn.norm_added_k) if joint else (None, "once", 0.0)
+    norms = [attn.norm_q, attn.norm_k] + ([attn.norm_added_q, attn.norm_added_k] if joint else [])
+    if video is None or text is None or not fusable(hidden_states, H, norms, D):
+        return None
+    w = lambda m: None if m is None else m.weight
+
+    single_text = attn.add_q_proj is None and encoder_hidden_states is not None
+    x = torch.cat([hidden_states, encoder_hidden_states], dim=1) if single_text else hidden_states
+    q_in, k_in, v_in = attn.to_q(x), attn.to_k(x), attn.to_v(x)
+    if not (q_in.is_contiguous() and k_in.is_contiguous() and v_in.is_contiguous()):
+        return None
+    B, S = x.shape[0], x.shape[1]
+    txt = encoder_hidden_states.shape[1] if encoder_hidden_states is not None else 0
+    N = S + txt if joint else S
+    rope, rope_rows = None, None
+    if image_rotary_emb is not None:
+        cos, sin = rope_tables_cossin(image_rotary_emb[0], image_rotary_emb[1], x.device)
+        rope_rows = S - txt if single_text else S
+        if cos.shape != (rope_rows, D) or sin.shape != (rope_rows, D):
+            return None
+        rope = ("cossin", cos, sin)
+    outs = [torch.empty(B, H, N, D, device=x.device, dtype=x.dtype) for _ in range(3)]
+    qkv_prologue(q_in, k_in, v_in, H, wq=w(attn.norm_q), wk=w(attn.norm_k), norm=video[0], rounding=video[1],
+                 eps=video[2], rope=rope, rope_rows=rope_rows, out=outs, out_seq_len=N)
+    if joint:
+        e = encoder_hidden_states
+        eq, ek, ev = attn.add_q_proj(e), attn.add_k_proj(e), attn.add_v_proj(e)
+        qkv_prologue(eq.contiguous(), ek.contiguous(), ev.contiguous(), H, wq=w(attn.norm_added_q),
+                     wk=w(attn.norm_added_k), norm=text[0], rounding=text[1], eps=text[2], out=outs,
+                     out_seq_len=N, out_row0=S)
+    return tuple(outs)
+
+
 def _rope_single(query, key, image_rotary_emb, txt_len):
     """RoPE on the video part of a single-stream sequence (text last) (:211-223)."""
     img_q, txt_q = query[:, :, :-txt_len], query[:, :, -txt_len:]
@@ -85,8 +145,15 @@ class HunyuanVideoAttnProcessor2_0_FlashAttention:
         if not hasattr(F, "scaled_dot_product_attention"):
             raise ImportError("HunyuanVideoAttnProcessor2_0_FlashAttention requires PyTorch 2.0.")
 
+    fused_prologue = True
+
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None,
                  image_rotary_emb=None):
+        qkv = (fused_hunyuan_qkv(attn, hidden_states, encoder_hidden_states, image_rotary_emb)
+               if self.fused_prologue else None)
+        if qkv is not None:
+            query, key, value = qkv
+            return self._attend_and_project(attn, query, key, value, encoder_hidden_states, attention_mask)
         if attn.add_q_proj is None and encoder_hidden_states is not None:
             hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
         query = _split_heads(attn, attn.to_q(hidden_states))
@@ -113,6 +180,9 @@ class HunyuanVideoAttnProcessor2_0_FlashAttention:
             query = torch.cat([query, eq], dim=2)
             key = torch.cat([key, ek], dim=2)
             value = torch.cat([value, ev], dim=2)
+        return self._attend_and_project(attn, query, key, value, encoder_hidden_states, attention_mask)
+
+    def _attend_and_project(self, attn, query, key, value, encoder_hidden_states, attention_mask):
         out = block_diagonal_attention(query, key, value, _valid_length(attention_mask, query.shape[2]))
         out = out.transpose(1, 2).flatten(2, 3).to(query.dtype)
         if encoder_hidden_states is not None:
@@ -139,6 +209,8 @@ class Hunyuan_SVGAttn_Processor2_0:
 
     first_layers_fp = 0
     first_times_fp = 0
+    # bf16 device inputs: projections' QK-norm, RoPE and text concat in fused HIP passes.
+    fused_prologue = True
 
     def __init__(self, layer_idx):
         self.layer_idx = layer_idx
@@ -204,13 +276,19 @@ class Hunyuan_SVGAttn_Processor2_0:
                  encoder_hidden_states: Optional[torch.Tensor] = None,
                  attention_mask: Optional[torch.Tensor] = None,
                  image_rotary_emb=None, timestep=None):
-        if attn.add_q_proj is None and encoder_hidden_states is not None:
-            hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
-        query, key, value = self.get_qkv(attn, hidden_states)
-        query, key, value = self.get_transpose_qkv(attn, query, key, value)
-        query, key = self.get_qk_norm(attn, query, key)
-        query, key = self.get_rotary_emb(attn, query, key, image_rotary_emb, encoder_hidden_states)
-        query, key, value = self.get_encoder_condition_and_concat(attn, query, key, value, encoder_hidden_states)
+        qkv = (fused_hunyuan_qkv(attn, hidden_states, encoder_hidden_states, image_rotary_emb)
+               if self.fused_prologue else None)
+        if qkv is not None:
+            query, key, value = qkv
+        else:
+            if attn.add_q_proj is None and encoder_hidden_states is not None:
+                hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
+            query, key, value = self.get_qkv(attn, hidden_states)
+            query, key, value = self.get_transpose_qkv(attn, query, key, value)
+            query, key = self.get_qk_norm(attn, query, key)
+            query, key = self.get_rotary_emb(attn, query, key, image_rotary_emb, encoder_hidden_states)
+            query, key, value = self.get_encoder_condition_and_concat(attn, query, key, value,
+                                                                      encoder_hidden_states)
         if attention_mask is None:
             attention_mask = torch.ones(query.shape[2], dtype=torch.bool, device=query.device)
         if timestep is None:

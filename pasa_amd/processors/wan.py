@@ -25,6 +25,8 @@ import torch.nn.functional as F
 
 from .. import density as _density
 from ..ops import pisa_pg_attention
+from ..prologue import qkv_prologue, rope_tables_complex
+from .qknorm import fusable, is_rmsnorm, norm_eps, rms_norm_once
 from .rope import apply_rotary_emb_complex
 from .timestep_hook import current_timestep, install_wan
 
@@ -42,6 +44,8 @@ class WanAttn_SVGAttn_Processor2_0:
     num_sampled_rows = 32
     attention_masks = None
     sparsity = 0
+    # bf16 device inputs: QK-norm, head split and RoPE in one HIP pass (pasa_amd.prologue).
+    fused_prologue = True
 
     def __init__(self, layer_idx):
         self.layer_idx = layer_idx
@@ -52,12 +56,52 @@ class WanAttn_SVGAttn_Processor2_0:
         return attn.to_q(hidden_states), attn.to_k(encoder_hidden_states), attn.to_v(encoder_hidden_states)
 
     def get_qk_norm(self, attn, query, key):
-        # RMSNorm over the full hidden width, before the head split (reference :122-136).
+        # RMSNorm over the full hidden width, before the head split, with the Triton
+        # rmsnorm's single rounding (reference :122-136).
         if attn.norm_q is not None:
-            query = attn.norm_q(query)
+            if not is_rmsnorm(attn.norm_q):
+                raise ValueError(f"Unsupported norm type: {type(attn.norm_q)}")
+            query = rms_norm_once(query, attn.norm_q.weight, norm_eps(attn.norm_q, query.dtype))
         if attn.norm_k is not None:
-            key = attn.norm_k(key)
+            if not is_rmsnorm(attn.norm_k):
+                raise ValueError(f"Unsupported norm type: {type(attn.norm_k)}")
+            key = rms_norm_once(key, attn.norm_k.weight, norm_eps(attn.norm_k, key.dtype))
         return query, key
+
+    def fused_qkv(self, attn, hidden_states, encoder_hidden_states, rotary_emb):
+        """get_qkv + get_qk_norm + get_transpose_qkv + get_rotary_emb in one kernel
+        pass; None when the inputs are outside what the kernel reproduces."""
+        H = attn.heads
+        C = hidden_states.shape[-1]
+        norms = (attn.norm_q, attn.norm_k)
+        if not all(m is None or is_rmsnorm(m) for m in norms):
+            return None
+        if not fusable(hidden_states, H, norms, C) or encoder_hidden_states.dtype != hidden_states.dtype:
+            return None
+        query = attn.to_q(hidden_states)
+        key, value = attn.to_k(encoder_hidden_states), attn.to_v(encoder_hidden_states)
+        if query.shape[-1] != C or key.shape[-1] != C or not (query.is_contiguous() and key.is_contiguous()
+                                                               and value.is_contiguous()):
+            return None
+        D = C // H
+        rope = None
+        if rotary_emb is not None:
+            re, im = rope_tables_complex(rotary_emb, query.device, query.shape[1], D // 2)
+            rope = ("complex", re, im)
+        wq = None if attn.norm_q is None else attn.norm_q.weight
+        wk = None if attn.norm_k is None else attn.norm_k.weight
+        eq = norm_eps(attn.norm_q, query.dtype) if attn.norm_q is not None else 0.0
+        ek = norm_eps(attn.norm_k, key.dtype) if attn.norm_k is not None else eq
+        row = lambda *ws: "row" if any(w is not None for w in ws) else None
+        if query.shape == key.shape and (wq is None or wk is None or eq == ek):
+            return qkv_prologue(query, key, value, H, wq=wq, wk=wk, norm=row(wq, wk), rounding="once",
+                                eps=eq if wq is not None else ek, rope=rope)
+        # cross-attention (different lengths) or different eps: Q alone, then K and V
+        (q, _, _) = qkv_prologue(query, None, None, H, wq=wq, norm=row(wq), rounding="once", eps=eq,
+                                 rope=rope)
+        (_, k, v) = qkv_prologue(None, key, value, H, wk=wk, norm=row(wk), rounding="once", eps=ek,
+                                 rope=rope if key.shape[1] == query.shape[1] else None)
+        return q, k, v
 
     def get_transpose_qkv(self, attn, query, key, value):
         query = query.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
@@ -93,10 +137,15 @@ class WanAttn_SVGAttn_Processor2_0:
         if encoder_hidden_states is None:
             encoder_hidden_states = hidden_states
 
-        query, key, value = self.get_qkv(attn, hidden_states, encoder_hidden_states)
-        query, key = self.get_qk_norm(attn, query, key)
-        query, key, value = self.get_transpose_qkv(attn, query, key, value)
-        query, key = self.get_rotary_emb(query, key, rotary_emb)
+        qkv = (self.fused_qkv(attn, hidden_states, encoder_hidden_states, rotary_emb)
+               if self.fused_prologue else None)
+        if qkv is not None:
+            query, key, value = qkv
+        else:
+            query, key, value = self.get_qkv(attn, hidden_states, encoder_hidden_states)
+            query, key = self.get_qk_norm(attn, query, key)
+            query, key, value = self.get_transpose_qkv(attn, query, key, value)
+            query, key = self.get_rotary_emb(query, key, rotary_emb)
 
         hidden_states_img = None
         if encoder_hidden_states_img is not None:  # I2V image branch (reference :195-208)

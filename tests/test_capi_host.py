@@ -201,3 +201,33 @@ def test_last_error_cleared_on_success(lib):
     assert lib.pasa_last_error() != b""
     assert lib.pasa_num_selected(0.5, 10) == 5
     assert lib.pasa_last_error() == b""
+
+
+def prologue(lib, **kw):
+    a = dict(xq=FAKE, xk=FAKE, xv=FAKE, q=FAKE + 1, k=FAKE + 2, v=FAKE + 3, wq=FAKE, wk=FAKE, B=1, S=100,
+             H=40, D=128, il=1, ol=0, OS=None, row0=0, norm=2, rnd=0, eps=1e-6, cos=FAKE, sin=FAKE, rope=2,
+             rr=None, dtype=0)
+    a.update(kw)
+    OS = a["S"] if a["OS"] is None else a["OS"]
+    rr = a["S"] if a["rr"] is None else a["rr"]
+    return lib.pasa_qkv_prologue(a["xq"], a["xk"], a["xv"], a["q"], a["k"], a["v"], a["wq"], a["wk"], a["B"],
+                                 a["S"], a["H"], a["D"], a["il"], a["ol"], OS, a["row0"], a["norm"], a["rnd"],
+                                 a["eps"], a["cos"], a["sin"], a["rope"], rr, a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(xq=None, xk=None, xv=None, q=None, k=None, v=None), -1),   # nothing to do
+    (dict(q=None), -1), (dict(xv=None), -1),                        # input without output and back
+    (dict(dtype=2), -7), (dict(D=96), -3), (dict(S=0), -2), (dict(H=0), -2), (dict(B=70000), -2),
+    (dict(H=65), -2),                                                # H*D > 8192
+    (dict(OS=99), -2), (dict(OS=150, row0=51), -2), (dict(row0=-1, OS=200), -2),
+    (dict(il=2), -9), (dict(ol=-1), -9), (dict(norm=3), -9), (dict(rnd=2), -9),
+    (dict(eps=float("nan")), -9), (dict(eps=-1.0), -9),
+    (dict(wq=None, wk=None), -1),                                    # a norm needs a weight
+    (dict(rope=3), -9), (dict(cos=None), -1), (dict(rr=101), -2), (dict(rr=-1), -2),
+    (dict(q=FAKE), -9),                                              # in place across layouts
+    (dict(q=FAKE, il=0, ol=0, OS=200), -9),                          # in place into a longer output
+])
+def test_prologue_validation(lib, kw, code):
+    assert prologue(lib, **kw) == code
+    assert lib.pasa_last_error()
