@@ -349,7 +349,7 @@ int pasa_qkv_prologue(const void* xq, const void* xk, const void* xv, void* q, v
     return fail(PASA_ERR_BAD_SHAPE, "rows [%lld, %lld) do not fit out_seq_len=%lld", (long long)out_row0,
                 (long long)(out_row0 + seq_len), (long long)out_seq_len);
   if (seq_len > INT64_MAX / batch / heads / head_dim || out_seq_len > INT64_MAX / batch / heads / head_dim ||
-      (seq_len + 3) / 4 > kMaxI32)
+      cdiv(cdiv(seq_len, 4), 8) * 24 > kMaxI32)
     return fail(PASA_ERR_OVERFLOW, "pasa_qkv_prologue: sizes overflow");
   if ((in_layout != PASA_LAYOUT_BHSD && in_layout != PASA_LAYOUT_BSHD) ||
       (out_layout != PASA_LAYOUT_BHSD && out_layout != PASA_LAYOUT_BSHD))

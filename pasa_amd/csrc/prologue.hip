@@ -40,15 +40,21 @@ constexpr int kLanesPerTok = 64;
 
 __device__ __forceinline__ float bf16r(float x) { return __uint_as_float(f32_to_bf16_bits(x) << 16); }
 
+// Workgroup n runs on XCD n % 8.  The three tensors of one token tile take slots
+// 3g, 3g+1, 3g+2 of the same XCD, so K's workgroup finds the rotary table Q's
+// workgroup just read in that XCD's L2.
 template <int CPT>
-__global__ __launch_bounds__(256) void k5_prologue(PrologueParams p) {
-  const int t = blockIdx.z;
+__global__ __launch_bounds__(256) void k5_prologue(PrologueParams p, int64_t tiles) {
+  const int64_t n = blockIdx.x;
+  const int64_t slot = n >> 3;
+  const int t = (int)(slot % 3);
+  const int64_t tile = (slot / 3) * 8 + (n & 7);
   const PrologueTensor T = p.t[t];
-  if (T.in == nullptr) return;  // tensor not requested (uniform over the workgroup)
+  if (T.in == nullptr || tile >= tiles) return;  // uniform over the workgroup
 
   const int tid = threadIdx.x;
   const int l = tid & (kLanesPerTok - 1);
-  const int64_t s = (int64_t)blockIdx.x * kTokPerWg + __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t s = tile * kTokPerWg + __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t b = blockIdx.y;
   const bool tok_ok = s < p.S;  // uniform over the wave
   const int D = p.D;
@@ -179,9 +185,10 @@ hipError_t launch_prologue(const PrologueParams& p, hipStream_t stream) {
   const int64_t cpt = (nc + kLanesPerTok - 1) / kLanesPerTok;
   if (cpt > kMaxCpt) return hipErrorInvalidValue;
   const int64_t tiles = (p.S + kTokPerWg - 1) / kTokPerWg;
-  if (tiles > 0x7fffffff || p.B > 65535) return hipErrorInvalidValue;
-  dim3 grid((unsigned)tiles, (unsigned)p.B, 3);
-#define PASA_K5(N) hipLaunchKernelGGL(k5_prologue<N>, grid, dim3(256), 0, stream, p)
+  const int64_t nwg = (tiles + 7) / 8 * 8 * 3;
+  if (nwg > 0x7fffffff || p.B > 65535) return hipErrorInvalidValue;
+  dim3 grid((unsigned)nwg, (unsigned)p.B, 1);
+#define PASA_K5(N) hipLaunchKernelGGL(k5_prologue<N>, grid, dim3(256), 0, stream, p, tiles)
   if (cpt <= 2) PASA_K5(2);
   else if (cpt <= 4) PASA_K5(4);
   else if (cpt <= 6) PASA_K5(6);
