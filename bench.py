@@ -158,6 +158,24 @@ def main() -> int:
     log(f"K5 prologue {k5:.3f} ms ({k5_gbps:.0f} GB/s algorithmic, {k5_bytes / 1e9:.2f} GB)")
     del xs, wts, ang, re_, im_
 
+    # Dense warm-up layers: K4's exact-tile path without selection vs PyTorch SDPA, one call each.
+    import torch.nn.functional as Fn
+    dense_flops = 4.0 * T * T * D * H
+    ops.dense_attention(q, k, v, scale=scale, out=bufs[0])
+    ka.record()
+    ops.dense_attention(q, k, v, scale=scale, out=bufs[0])
+    kb.record()
+    torch.cuda.synchronize()
+    kd_ms = ka.elapsed_time(kb)
+    Fn.scaled_dot_product_attention(q, k, v, scale=scale)
+    ka.record()
+    Fn.scaled_dot_product_attention(q, k, v, scale=scale)
+    kb.record()
+    torch.cuda.synchronize()
+    sdpa_ms = ka.elapsed_time(kb)
+    log(f"dense attention {kd_ms:.1f} ms ({dense_flops / kd_ms / 1e9:.0f} TFLOP/s); "
+        f"PyTorch SDPA {sdpa_ms:.1f} ms ({dense_flops / sdpa_ms / 1e9:.0f} TFLOP/s)")
+
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
@@ -229,6 +247,9 @@ def main() -> int:
                        "inv_ms": round(k1i, 4), "inv_GBps": round(k1i_gbps, 1),
                        "frac_of_hbm_peak_fwd": round(k1f_gbps / PEAK_HBM_GBPS, 4)},
         "k2_GBps_algorithmic": round(k2_bytes / (k2 * 1e-3) / 1e9, 1),
+        "dense_attention": {"ms": round(kd_ms, 3), "TFLOPs": round(dense_flops / kd_ms / 1e9, 1),
+                            "torch_sdpa_ms": round(sdpa_ms, 3),
+                            "note": "warm-up layers: every key block exact, no selection; one call each"},
         "k5_prologue": {"ms": round(k5, 4), "GBps": round(k5_gbps, 1), "bytes": k5_bytes,
                         "frac_of_hbm_peak": round(k5_gbps / PEAK_HBM_GBPS, 4),
                         "mode": "Wan: RMSNorm over H*D (one rounding) + head split + complex fp64 RoPE, Q/K/V"},

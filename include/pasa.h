@@ -188,6 +188,18 @@ int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const v
                             int64_t text_valid, int64_t head_dim, int64_t block_size,
                             int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* stream);
 
+/* Dense softmax attention, o = softmax(scale * q k^T) v, on K4's exact-tile path
+ * (every key block exact; no statistics, selection or correction).  With a text
+ * segment (text_len > 0) the attention is block-diagonal over [0, seq_len -
+ * text_len + text_valid) and the padding rows after it, the cu_seqlens semantics
+ * of the dense HunyuanVideo path.  bf16, head_dim 128; no workspace.
+ * Replaces: the dense warm-up branch of the processors, flash_attention /
+ * F.scaled_dot_product_attention (svg/models/wan/attention.py:299-301, :378-379;
+ * svg/models/hyvideo/attention.py:450-476, :671-672). */
+int pasa_dense_attn(const void* q, const void* k, const void* v, void* o, double scale,
+                    int64_t bh, int64_t seq_len, int64_t text_len, int64_t text_valid,
+                    int64_t head_dim, int dtype, void* stream);
+
 /* ---- Processor prologue (K5) ------------------------------------------------ */
 
 typedef enum {

@@ -60,6 +60,7 @@ SIGNATURES = {
     "pasa_pack_phase2": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "pasa_sparse_attn_packed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
+    "pasa_dense_attn": (_int, [_vp, _vp, _vp, _vp, _dbl, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "pasa_qkv_prologue": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int,
                                  _i64, _i64, _int, _int, _dbl, _vp, _vp, _int, _i64, _int, _vp]),
 }

@@ -322,6 +322,27 @@ int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* k
                                  dtype, stream);
 }
 
+int pasa_dense_attn(const void* q, const void* k, const void* v, void* o, double scale, int64_t bh,
+                    int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim, int dtype,
+                    void* stream) {
+  if (!q || !k || !v || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_dense_attn: NULL pointer");
+  if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_dense_attn: only bf16 inputs are supported");
+  if (head_dim != 128) return fail(PASA_ERR_HEAD_DIM, "pasa_dense_attn: head_dim %lld != 128", (long long)head_dim);
+  int rc;
+  if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
+  if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
+  if ((rc = check_text(seq_len, text_len, head_dim))) return rc;
+  if (text_valid < 0 || text_valid > text_len)
+    return fail(PASA_ERR_TEXT_SEGMENT, "text_valid=%lld must be in [0, text_len=%lld]", (long long)text_valid,
+                (long long)text_len);
+  if (!std::isfinite(scale) || !(scale > 0.0)) return fail(PASA_ERR_BAD_ARG, "scale must be finite and > 0");
+  const int64_t grid = 8 * bh * cdiv(cdiv(seq_len - text_len, 128), 8) + 8 * cdiv(bh * (cdiv(text_len, 128) + 1), 8);
+  if (grid > kMaxI32) return fail(PASA_ERR_OVERFLOW, "grid too large");
+  return launch_status(pasa::launch_dense_attn(q, k, v, o, (float)scale, (int)bh, (int)(seq_len - text_len),
+                                               (int)text_len, (int)text_valid, (hipStream_t)stream),
+                       "pasa_dense_attn");
+}
+
 int pasa_qkv_prologue(const void* xq, const void* xk, const void* xv, void* q, void* k, void* v,
                       const void* wq, const void* wk, int64_t batch, int64_t seq_len, int64_t heads,
                       int64_t head_dim, int in_layout, int out_layout, int64_t out_seq_len, int64_t out_row0,

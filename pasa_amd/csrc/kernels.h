@@ -39,6 +39,13 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
                               int bh, int T, int text, int text_valid, int D, int BT, int NS,
                               int gamma_literal, hipStream_t stream);
 
+// Dense softmax attention with K4's phase-1 machinery (every key block exact, no
+// selection, no correction), D = 128.  T video rows, then `text` rows of which the
+// first text_valid are the prompt: rows attend within [0, T + text_valid) or within
+// the padding [T + text_valid, T + text).
+hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* o, float scale, int bh,
+                             int T, int text, int text_valid, hipStream_t stream);
+
 // ---- K5: processor prologue (RMSNorm + rotary embedding + head-major layout) ----
 constexpr int kNormHead = 1;       // RMSNorm over each head's D channels, weight [D]
 constexpr int kNormRow = 2;        // RMSNorm over the token's H*D channels, weight [H*D]

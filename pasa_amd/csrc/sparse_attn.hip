@@ -570,7 +570,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
                         const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
                         const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o,
                         float scale, float c, int T, int NT, int NG, int NW, int xcd_chunk,
-                        int gamma_literal, int text, int text_valid, int n_text_wg, int nbh) {
+                        int gamma_literal, int text, int text_valid, int n_text_wg, int nbh,
+                        int all_tiles) {
   using C = K4D<BT>;
   using PK = typename C::PK;
   constexpr int D = 128;
@@ -699,8 +700,11 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     vofs[et] = (4 * (g16 >> 1) + (i16 >> 2)) * 256 +
                ((4 * (et ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
 
+  // all_tiles (dense attention): every key block is exact, no selection is read and
+  // there is no correction term.
   int wsel = 0;
-  uint32_t bits = (!dense && NW > 0) ? mrow[0] : 0u;
+  int jall = 0;
+  uint32_t bits = (!dense && !all_tiles && NW > 0) ? mrow[0] : 0u;
   auto next_selected = [&]() -> int {
     while (bits == 0u) {
       if (++wsel >= NW) return -1;
@@ -717,7 +721,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   int tt = 0;
   auto next_tile = [&](int& nv) -> int {
     if (!dense) {
-      const int j = next_selected();
+      const int j = all_tiles ? (jall < NT ? jall++ : -1) : next_selected();
       if (j >= 0) {
         nv = min(BT, T - j * BT);
         return j * BT;
@@ -854,7 +858,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const u32x4_t pd = make_rsrc_words(pack + (int64_t)bh * NG * PK::BYTES, (uint32_t)(NG * PK::BYTES));
   const unsigned char* Pvt = Vs + PK::VT_OFF;
   const int pv_base = PadTile<kGroup>::frag_base(l32, h);
-  const int ng_run = dense ? 0 : NG;  // text rows have no correction term
+  const int ng_run = (dense || all_tiles) ? 0 : NG;  // text rows and dense attention: no correction term
   // Groups with at least one unselected in-range block, in ascending order.
   auto approx_of = [&](int g) -> uint32_t {
     const int nin = min(kGroup, NT - g * kGroup);
@@ -1051,10 +1055,10 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
                      b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
   if (D == 128 && BT == 128)
     hipLaunchKernelGGL((k4_sparse_attn_dma<128>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh, 0);
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k4_sparse_attn_dma<64>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh, 0);
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
   else if (D == 64 && BT == 64)
@@ -1062,6 +1066,21 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
   else
     return hipErrorInvalidValue;
 #undef PASA_K4_LAUNCH
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* o, float scale, int bh,
+                             int T, int text, int text_valid, hipStream_t stream) {
+  constexpr int BT = 128;
+  if (T < 1 || text < 0 || text_valid < 0 || text_valid > text) return hipErrorInvalidValue;
+  const int NT = (T + BT - 1) / BT;
+  const int xcd_chunk = (NT + 7) / 8;
+  const int text_qtiles = (text_valid + BT - 1) / BT + (text - text_valid + BT - 1) / BT;
+  const int n_text_wg = (bh * text_qtiles + 7) / 8 * 8;
+  dim3 grid(n_text_wg + 8 * bh * xcd_chunk);
+  hipLaunchKernelGGL((k4_sparse_attn_dma<BT>), grid, dim3(K4D<BT>::THREADS), 0, stream, (const uint16_t*)q,
+                     (const uint16_t*)k, (const uint16_t*)v, nullptr, nullptr, (uint16_t*)o, scale,
+                     scale * kLog2e, T, NT, 0, 0, xcd_chunk, 1, text, text_valid, n_text_wg, bh, 1);
   return hipGetLastError();
 }
 

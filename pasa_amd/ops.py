@@ -8,6 +8,7 @@ processors call it unchanged.  Each stage is also exposed on its own:
 * ``select_blocks``      K3  (reference :365-375)
 * ``select_from_scores`` K3's top-k on given scores (bit-exact parity entry)
 * ``sparse_attn``        K4  (reference :135-262)
+* ``dense_attention``    K4's exact-tile path without selection (dense warm-up layers)
 
 All device work goes through libpasa_amd.so (ctypes, ``pasa_amd._lib``).  This
 module allocates outputs and workspace with torch's caching allocator and passes
@@ -180,6 +181,25 @@ def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockS
     text rows are dense within their segment."""
     pack = pack_phase2(q, stats, block_size, text_tokens)
     return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out, text_tokens, text_valid)
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
+                    text_tokens: int = 0, text_valid: Optional[int] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense softmax attention on K4's exact-tile path (bf16, head_dim 128), for the
+    processors' warm-up layers (reference flash_attention, svg/models/wan/attention.py:299-301,
+    svg/models/hyvideo/attention.py:459-476).  With ``text_tokens`` / ``text_valid``
+    the attention is block-diagonal over [0, T - text_tokens + text_valid) and the
+    rest (the dense HunyuanVideo path's cu_seqlens).  q, k, v: [B, H, T, 128]."""
+    _check_device(q, k, v)
+    B, H, T, D = q.shape
+    scale = D ** -0.5 if scale is None else scale
+    o = torch.empty_like(v) if out is None else out
+    _check_device(o)
+    tv = text_tokens if text_valid is None else text_valid
+    _lib.call("pasa_dense_attn", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), float(scale), B * H, T,
+              int(text_tokens), int(tv), D, _DTYPES.get(q.dtype, -1), _stream(q))
+    return o
 
 
 def pisa_pg_attention(

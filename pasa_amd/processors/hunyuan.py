@@ -41,6 +41,7 @@ from .. import density as _density
 from ..ops import pisa_pg_attention
 from ..placement import hunyuan_hidden_states_placement, hunyuan_sparse_head_placement
 from ..prologue import qkv_prologue, rope_tables_cossin
+from . import dense as _dense
 from .qknorm import fusable, module_rounding, norm_eps
 from .rope import apply_rotary_emb_cos_sin
 from .timestep_hook import current_timestep, install_hunyuan
@@ -51,16 +52,9 @@ def _split_heads(attn, x):
 
 
 def block_diagonal_attention(query, key, value, valid: int):
-    """softmax attention restricted to [0, valid) x [0, valid) and [valid, N) x [valid, N)."""
-    N = query.shape[2]
-    if valid >= N:
-        return F.scaled_dot_product_attention(query, key, value, dropout_p=0.0, is_causal=False)
-    out = torch.empty_like(query)
-    for a, b in ((0, valid), (valid, N)):
-        if b > a:
-            out[:, :, a:b] = F.scaled_dot_product_attention(query[:, :, a:b], key[:, :, a:b], value[:, :, a:b],
-                                                            dropout_p=0.0, is_causal=False)
-    return out
+    """softmax attention restricted to [0, valid) x [0, valid) and [valid, N) x [valid, N)
+    (the HIP dense path for bf16 device tensors, see ``processors.dense``)."""
+    return _dense.attention(query, key, value, valid)
 
 
 def _valid_length(attention_mask, n: int) -> int:

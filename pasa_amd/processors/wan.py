@@ -26,6 +26,7 @@ import torch.nn.functional as F
 from .. import density as _density
 from ..ops import pisa_pg_attention
 from ..prologue import qkv_prologue, rope_tables_complex
+from . import dense as _dense
 from .qknorm import fusable, is_rmsnorm, norm_eps, rms_norm_once
 from .rope import apply_rotary_emb_complex
 from .timestep_hook import current_timestep, install_wan
@@ -167,8 +168,9 @@ class WanAttn_SVGAttn_Processor2_0:
         return self.get_o(attn, query, hidden_states, hidden_states_img)
 
     def flash_attention(self, query, key, value):
-        """Dense attention (reference :298-301), PyTorch-ROCm SDPA."""
-        return F.scaled_dot_product_attention(query, key, value, dropout_p=0.0, is_causal=False)
+        """Dense attention (reference :299-301): the HIP exact-tile path for bf16 device
+        tensors with head_dim 128, else PyTorch SDPA (``processors.dense``)."""
+        return _dense.attention(query, key, value)
 
     def attention_core_logic(self, query, key, value, timestep):  # pragma: no cover - abstract
         raise NotImplementedError

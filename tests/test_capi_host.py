@@ -231,3 +231,18 @@ def prologue(lib, **kw):
 def test_prologue_validation(lib, kw, code):
     assert prologue(lib, **kw) == code
     assert lib.pasa_last_error()
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(o=None), -1), (dict(q=None), -1), (dict(dtype=2), -7), (dict(D=64), -3), (dict(T=0), -2),
+    (dict(bh=0), -2), (dict(text=1000), -10), (dict(text=-1), -10), (dict(text=10, tv=11), -10),
+    (dict(text=10, tv=-1), -10), (dict(scale=0.0), -9), (dict(scale=float("inf")), -9),
+    (dict(T=(1 << 24) - 100), -6),
+])
+def test_dense_attn_validation(lib, kw, code):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, scale=0.1, bh=2, T=1000, text=0, tv=None, D=128, dtype=0)
+    a.update(kw)
+    tv = a["text"] if a["tv"] is None else a["tv"]
+    assert lib.pasa_dense_attn(a["q"], a["k"], a["v"], a["o"], a["scale"], a["bh"], a["T"], a["text"], tv, a["D"],
+                               a["dtype"], None) == code
+    assert lib.pasa_last_error()

@@ -376,3 +376,41 @@ def test_end_to_end_c3_one_head_text_segment(device):
     st = ops.block_stats(qd, kd, vd, wl.block_size, 32, text_tokens=wl.text_tokens)
     idx = ops.select_blocks(st, wl.density, wl.op_scale).idx.cpu()
     check_end_to_end(o, q, k, v, wl, idx, None, "c3 one head")
+
+
+# ------------------------------------------------------------ dense warm-up --
+
+@pytest.mark.parametrize("heads,T,text,valid", [(2, 600, 0, None), (1, 129, 0, None), (2, 1000, 100, 37),
+                                                 (1, 700, 300, 0), (2, 384, 128, 128)])
+def test_dense_attention(device, heads, T, text, valid):
+    """K4's exact-tile path without selection: softmax attention, block-diagonal with a
+    text segment; at the floor set by rounding P to bf16 (the oracle at density 1 with
+    the reference's roundings)."""
+    say(f"[dense] heads={heads} T={T} text={text} valid={valid}")
+    g = torch.Generator().manual_seed(T + text)
+    q, k, v = (torch.randn(1, heads, T, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+    o = ops.dense_attention(q.to(device), k.to(device), v.to(device), text_tokens=text, text_valid=valid).cpu()
+    es = O.effective_scale(128 ** -0.5)
+    seg = T - text + (text if valid is None else valid)
+    qd, kd, vd = q.double(), k.double(), v.double()
+    ref = torch.empty(1, heads, T, 128, dtype=torch.float64)
+    ref[..., :seg, :] = O.dense_attention(qd[..., :seg, :], kd[..., :seg, :], vd[..., :seg, :], es)
+    if seg < T:
+        ref[..., seg:, :] = O.dense_attention(qd[..., seg:, :], kd[..., seg:, :], vd[..., seg:, :], es)
+    rp = O.pisa_pg_attention(q.float(), k.float(), v.float(), 1.0, 128, 32, 128 ** -0.5, ref_precision=True,
+                             text_tokens=text, text_valid=valid)
+    floor = O.parity_metrics(rp, ref)
+    check_parity(o, ref, f"dense T={T} text={text} valid={valid}", floor)
+
+
+def test_processor_dense_split_matches_two_sdpa_calls(device):
+    """processors.dense.attention with a cu_seqlens split equals two dense attentions."""
+    from pasa_amd.processors import dense as DN
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(1, 2, 500, 128, generator=g).to(torch.bfloat16).to(device) for _ in range(3))
+    o = DN.attention(q, k, v, 421).float().cpu()
+    ref = torch.cat([torch.nn.functional.scaled_dot_product_attention(q[:, :, :421].float(), k[:, :, :421].float(),
+                                                                       v[:, :, :421].float()),
+                     torch.nn.functional.scaled_dot_product_attention(q[:, :, 421:].float(), k[:, :, 421:].float(),
+                                                                       v[:, :, 421:].float())], dim=2).cpu()
+    check_parity(o, ref.double(), "processor dense split")
