@@ -564,14 +564,16 @@ __device__ __forceinline__ void barrier_lds_reads_done() {
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
-template <int BT>
+// ALL: dense attention (every key block exact, no selection read, no correction); a
+// separate instantiation so that profiles tell the two launches apart.
+template <int BT, bool ALL>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
 void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                         const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
                         const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o,
                         float scale, float c, int T, int NT, int NG, int NW, int xcd_chunk,
-                        int gamma_literal, int text, int text_valid, int n_text_wg, int nbh,
-                        int all_tiles) {
+                        int gamma_literal, int text, int text_valid, int n_text_wg, int nbh) {
+  constexpr bool all_tiles = ALL;
   using C = K4D<BT>;
   using PK = typename C::PK;
   constexpr int D = 128;
@@ -700,8 +702,6 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     vofs[et] = (4 * (g16 >> 1) + (i16 >> 2)) * 256 +
                ((4 * (et ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
 
-  // all_tiles (dense attention): every key block is exact, no selection is read and
-  // there is no correction term.
   int wsel = 0;
   int jall = 0;
   uint32_t bits = (!dense && !all_tiles && NW > 0) ? mrow[0] : 0u;
@@ -1054,11 +1054,11 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
   hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid_video, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
                      b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
   if (D == 128 && BT == 128)
-    hipLaunchKernelGGL((k4_sparse_attn_dma<128>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh, 0);
+    hipLaunchKernelGGL((k4_sparse_attn_dma<128, false>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b, cc,
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
   else if (D == 128 && BT == 64)
-    hipLaunchKernelGGL((k4_sparse_attn_dma<64>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh, 0);
+    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b, cc,
+                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
   else if (D == 64 && BT == 64)
@@ -1078,9 +1078,9 @@ hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* 
   const int text_qtiles = (text_valid + BT - 1) / BT + (text - text_valid + BT - 1) / BT;
   const int n_text_wg = (bh * text_qtiles + 7) / 8 * 8;
   dim3 grid(n_text_wg + 8 * bh * xcd_chunk);
-  hipLaunchKernelGGL((k4_sparse_attn_dma<BT>), grid, dim3(K4D<BT>::THREADS), 0, stream, (const uint16_t*)q,
+  hipLaunchKernelGGL((k4_sparse_attn_dma<BT, true>), grid, dim3(K4D<BT>::THREADS), 0, stream, (const uint16_t*)q,
                      (const uint16_t*)k, (const uint16_t*)v, nullptr, nullptr, (uint16_t*)o, scale,
-                     scale * kLog2e, T, NT, 0, 0, xcd_chunk, 1, text, text_valid, n_text_wg, bh, 1);
+                     scale * kLog2e, T, NT, 0, 0, xcd_chunk, 1, text, text_valid, n_text_wg, bh);
   return hipGetLastError();
 }
 
