@@ -158,6 +158,28 @@ def main() -> int:
     log(f"K5 prologue {k5:.3f} ms ({k5_gbps:.0f} GB/s algorithmic, {k5_bytes / 1e9:.2f} GB)")
     del xs, wts, ang, re_, im_
 
+    # Placement folded into K2/K4 (frame-major q, k, v read through the token-major view)
+    # against K1 forward + the call + K1 inverse, one call each after a warm-up.
+    pl = ops.Placement(F, P, None)
+    run_placed = lambda: ops.pisa_pg_attention(q, k, v, wl.density, block_size=BT, scale=scale, text_tokens=X,
+                                               placement=pl)
+
+    def run_separate():
+        placement.permute([q, k, v], bufs, F, P, X)
+        ot = ops.pisa_pg_attention(bufs[0], bufs[1], bufs[2], wl.density, block_size=BT, scale=scale,
+                                   text_tokens=X)
+        placement.permute([ot], [out], F, P, X, inverse=True)
+
+    placed_ms = {}
+    for name, fn in (("folded", run_placed), ("k1_separate", run_separate)):
+        fn()
+        ka.record()
+        fn()
+        kb.record()
+        torch.cuda.synchronize()
+        placed_ms[name] = ka.elapsed_time(kb)
+    log(f"placed call {placed_ms['folded']:.3f} ms; K1 + call + K1 inverse {placed_ms['k1_separate']:.3f} ms")
+
     # Dense warm-up layers: K4's exact-tile path without selection vs PyTorch SDPA, one call each.
     import torch.nn.functional as Fn
     dense_flops = 4.0 * T * T * D * H
@@ -247,6 +269,8 @@ def main() -> int:
                        "inv_ms": round(k1i, 4), "inv_GBps": round(k1i_gbps, 1),
                        "frac_of_hbm_peak_fwd": round(k1f_gbps / PEAK_HBM_GBPS, 4)},
         "k2_GBps_algorithmic": round(k2_bytes / (k2 * 1e-3) / 1e9, 1),
+        "placement_folded": {"ms": round(placed_ms["folded"], 3), "k1_separate_ms": round(placed_ms["k1_separate"], 3),
+                             "note": "frame-major q/k/v: placement folded into K2/K4 vs K1 + call + K1 inverse"},
         "dense_attention": {"ms": round(kd_ms, 3), "TFLOPs": round(dense_flops / kd_ms / 1e9, 1),
                             "torch_sdpa_ms": round(sdpa_ms, 3),
                             "note": "warm-up layers: every key block exact, no selection; one call each"},

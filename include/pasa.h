@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 3
+#define PASA_ABI_VERSION 4
 
 typedef enum {
   PASA_OK = 0,
@@ -187,6 +187,40 @@ int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const v
                             void* o, double scale, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t text_valid, int64_t head_dim, int64_t block_size,
                             int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* stream);
+
+/* ---- Token-major view of frame-major tensors -------------------------------- */
+
+/* The HunyuanVideo placement (pasa_permute's forward map) as a view: for a head
+ * whose flag is set, logical row p*F + f of the first F*P rows of a slice (token p
+ * of frame f, token-major) is stored at row f*P + p (frame-major); the rows after
+ * them (the text tail) and every row of a head whose flag is 0 are in place. */
+typedef struct {
+  int64_t num_frame;               /* F */
+  int64_t frame_size;              /* P, tokens per frame; F*P = seq_len - text_len <= 2^24 */
+  const int32_t* head_is_temporal; /* device int32 [heads]; NULL: every head permuted      */
+  int64_t heads;                   /* slice s is head s % heads                            */
+} pasa_placement_t;
+
+/* pasa_block_stats and pasa_sparse_attn_packed on frame-major q, k, v (o written
+ * frame-major): the result equals permuting q, k, v to token-major (pasa_permute),
+ * running the unplaced entry points and permuting o back, without the three extra
+ * passes over HBM.  head_dim 128, block_size 128; arguments otherwise as for the
+ * unplaced entry points.
+ * Replaces: hunyuan_sparse_head_placement / hunyuan_hidden_states_placement around the
+ * attention call (svg/models/hyvideo/placement.py:124-153, :360-387;
+ * svg/models/hyvideo/attention.py:412-446). */
+int pasa_block_stats_placed(const void* q, const void* k, const void* v,
+                            float* qc, float* kc, float* vc, float* hnorm, float* hgroup,
+                            int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
+                            int64_t block_size, int64_t group_size,
+                            const pasa_placement_t* placement, int dtype, void* stream);
+int pasa_sparse_attn_packed_placed(const void* q, const void* k, const void* v, const void* pack,
+                                   size_t pack_bytes, const int32_t* idx, const uint32_t* selmask,
+                                   void* o, double scale, int64_t bh, int64_t seq_len,
+                                   int64_t text_len, int64_t text_valid, int64_t head_dim,
+                                   int64_t block_size, int64_t group_size, int64_t ns,
+                                   int gamma_literal, const pasa_placement_t* placement,
+                                   int dtype, void* stream);
 
 /* Dense softmax attention, o = softmax(scale * q k^T) v, on K4's exact-tile path
  * (every key block exact; no statistics, selection or correction).  With a text

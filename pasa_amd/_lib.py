@@ -40,6 +40,14 @@ _int = ctypes.c_int
 _dbl = ctypes.c_double
 _sz = ctypes.c_size_t
 
+class Placement(ctypes.Structure):
+    """pasa_placement_t: the token-major view of frame-major slices."""
+    _fields_ = [("num_frame", ctypes.c_int64), ("frame_size", ctypes.c_int64),
+                ("head_is_temporal", ctypes.c_void_p), ("heads", ctypes.c_int64)]
+
+
+_pl = ctypes.POINTER(Placement)
+
 # name -> (restype, argtypes); mirrors include/pasa.h exactly.
 SIGNATURES = {
     "pasa_abi_version": (_int, []),
@@ -60,12 +68,16 @@ SIGNATURES = {
     "pasa_pack_phase2": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "pasa_sparse_attn_packed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
+    "pasa_block_stats_placed": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                       _i64, _pl, _int, _vp]),
+    "pasa_sparse_attn_packed_placed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
+                                              _i64, _i64, _i64, _i64, _i64, _int, _pl, _int, _vp]),
     "pasa_dense_attn": (_int, [_vp, _vp, _vp, _vp, _dbl, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "pasa_qkv_prologue": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int,
                                  _i64, _i64, _int, _int, _dbl, _vp, _vp, _int, _i64, _int, _vp]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class PasaError(RuntimeError):

@@ -217,11 +217,13 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 // chunk c of row r at c ^ 4(r & 3)); Q rows go to registers.  Block j+1's loads are in
 // flight while block j is reduced.  H_j = K^T V reads both MFMA operands with the
 // transposing ds_read_b64_tr_b16 (K^T as A, V as B; the same token order in both).
+// PERM: q, k, v are frame-major; the statistics are those of their token-major view (rm).
+template <bool PERM>
 __global__ __launch_bounds__(256, 1) void k2_block_stats_dma(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, float* __restrict__ qc, float* __restrict__ kc,
     float* __restrict__ vc, float* __restrict__ hnorm, float* __restrict__ hgroup, int T, int Tslice,
-    int NT, int G) {
+    int NT, int G, RowMap rm) {
   constexpr int D = 128;
   constexpr int BT = 128;
   constexpr int TILE = BT * 256;
@@ -255,7 +257,22 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats_dma(
   const int lrow = lane >> 4;
   const int lch = lane & 15;
   const uint32_t t_lane = (uint32_t)((4 * wave + lrow) * 256 + ((lch ^ (4 * lrow)) << 4));
+  const bool perm = PERM && slice_permuted(rm, bh);
+  // Stored row of logical row r (rows past T are not permuted and read as zero).
+  auto st = [&](int r) -> uint32_t { return (uint32_t)(perm ? map_row(r, rm) : r); };
   auto load_kv = [&](int buf, int j) {
+    if (perm) {
+      uint32_t off[BT / 16];
+#pragma unroll
+      for (int n = 0; n < BT / 16; ++n) off[n] = st(j * BT + 16 * n + 4 * wave + lrow) * 256u + (t_lane & 255u);
+#pragma unroll
+      for (int n = 0; n < BT / 16; ++n)
+        dma_load16_lds(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off[n], 0u);
+#pragma unroll
+      for (int n = 0; n < BT / 16; ++n)
+        dma_load16_lds(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off[n], 0u);
+      return;
+    }
     const uint32_t soff = (uint32_t)j * BT * 256u;
 #pragma unroll
     for (int n = 0; n < BT / 16; ++n)
@@ -270,7 +287,7 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats_dma(
   auto load_q = [&](uint4 (&qv)[BT / 16], int j) {
 #pragma unroll
     for (int p = 0; p < BT / 16; ++p)
-      qv[p] = buf_load16(qr, ((uint32_t)(j * BT + 16 * p + prow) * D + pc * 8) * 2u);
+      qv[p] = buf_load16(qr, (st(j * BT + 16 * p + prow) * D + pc * 8) * 2u);
   };
 
   // Transposing operand reads: lane gets feature 32 ft + l32, tokens 4h + {0..3} (lo)
@@ -428,16 +445,20 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats_dma(
 
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
-                              int BT, int G, hipStream_t stream) {
+                              int BT, int G, const RowMap* rm, hipStream_t stream) {
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + G - 1) / G;
   dim3 grid(NG, bh);
   auto a = (const uint16_t*)q;
   auto b = (const uint16_t*)k;
   auto c = (const uint16_t*)v;
-  if (D == 128 && BT == 128)
-    hipLaunchKernelGGL(k2_block_stats_dma, grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm, hgroup,
-                       T, Tslice, NT, G);
+  if (rm != nullptr) {  // token-major view of frame-major slices: D = 128, BT = 128 only
+    if (D != 128 || BT != 128) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k2_block_stats_dma<true>, grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm, hgroup,
+                       T, Tslice, NT, G, *rm);
+  } else if (D == 128 && BT == 128)
+    hipLaunchKernelGGL(k2_block_stats_dma<false>, grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
+                       hgroup, T, Tslice, NT, G, RowMap{});
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k2_block_stats<128, 64>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
                        hnorm, hgroup, T, Tslice, NT, G);

@@ -152,9 +152,10 @@ int pasa_permute(const void* src0, const void* src1, const void* src2, void* dst
                        "pasa_permute");
 }
 
-int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
-                     float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
-                     int64_t head_dim, int64_t block_size, int64_t group_size, int dtype, void* stream) {
+static int block_stats_impl(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
+                            float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
+                            int64_t head_dim, int64_t block_size, int64_t group_size, int dtype,
+                            const pasa::RowMap* rm, void* stream) {
   if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
   if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_block_stats: only bf16 inputs are supported");
   int rc;
@@ -166,8 +167,45 @@ int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, flo
   if (group_size <= 0 || group_size > 1 << 20) return fail(PASA_ERR_GROUP_SIZE, "group_size %lld must be in [1, 2^20]", (long long)group_size);
   return launch_status(pasa::launch_block_stats(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh,
                                                 (int)(seq_len - text_len), (int)seq_len, (int)head_dim,
-                                                (int)block_size, (int)group_size, (hipStream_t)stream),
+                                                (int)block_size, (int)group_size, rm, (hipStream_t)stream),
                        "pasa_block_stats");
+}
+
+int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
+                     float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
+                     int64_t head_dim, int64_t block_size, int64_t group_size, int dtype, void* stream) {
+  return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
+                          group_size, dtype, nullptr, stream);
+}
+
+// The placement's row map, after checking it fits the slices it will address.
+static int check_placement(const pasa_placement_t* pl, int64_t bh, int64_t seq_len, int64_t text_len,
+                           int64_t head_dim, int64_t block_size, pasa::RowMap* rm) {
+  if (!pl) return fail(PASA_ERR_NULL_POINTER, "placement is NULL");
+  if (head_dim != 128) return fail(PASA_ERR_HEAD_DIM, "the placed kernels need head_dim 128 (got %lld)", (long long)head_dim);
+  if (block_size != 128) return fail(PASA_ERR_BLOCK_SIZE, "the placed kernels need block_size 128 (got %lld)", (long long)block_size);
+  if (pl->num_frame < 1 || pl->frame_size < 1 || pl->num_frame > (1 << 24) || pl->frame_size > (1 << 24) ||
+      pl->num_frame * pl->frame_size != seq_len - text_len)
+    return fail(PASA_ERR_BAD_SHAPE, "num_frame*frame_size=%lld*%lld must equal seq_len - text_len = %lld",
+                (long long)pl->num_frame, (long long)pl->frame_size, (long long)(seq_len - text_len));
+  if (pl->num_frame * pl->frame_size > (1 << 24))
+    return fail(PASA_ERR_OVERFLOW, "num_frame*frame_size exceeds 2^24 rows");
+  if (pl->heads < 1 || bh % pl->heads != 0)
+    return fail(PASA_ERR_BAD_SHAPE, "heads=%lld must divide bh=%lld", (long long)pl->heads, (long long)bh);
+  *rm = pasa::RowMap{(int)pl->num_frame, (int)pl->frame_size, 1.0f / (float)pl->num_frame, pl->head_is_temporal,
+                     (int)pl->heads};
+  return PASA_OK;
+}
+
+int pasa_block_stats_placed(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
+                            float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
+                            int64_t head_dim, int64_t block_size, int64_t group_size,
+                            const pasa_placement_t* placement, int dtype, void* stream) {
+  pasa::RowMap rm;
+  int rc;
+  if ((rc = check_placement(placement, bh, seq_len, text_len, head_dim, block_size, &rm))) return rc;
+  return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
+                          group_size, dtype, &rm, stream);
 }
 
 size_t pasa_select_workspace_bytes(int64_t bh, int64_t num_blocks) {
@@ -285,11 +323,11 @@ static int check_attn_args(const void* q, const void* k, const void* v, const in
   return PASA_OK;
 }
 
-int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack, size_t pack_bytes,
-                            const int32_t* idx, const uint32_t* selmask, void* o, double scale, int64_t bh,
-                            int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim,
-                            int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype,
-                            void* stream) {
+static int sparse_attn_packed_impl(const void* q, const void* k, const void* v, const void* pack,
+                                   size_t pack_bytes, const int32_t* idx, const uint32_t* selmask, void* o,
+                                   double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t text_valid,
+                                   int64_t head_dim, int64_t block_size, int64_t group_size, int64_t ns,
+                                   int gamma_literal, int dtype, const pasa::RowMap* rm, void* stream) {
   int rc;
   if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, text_valid, head_dim,
                             block_size, group_size, ns, gamma_literal, dtype)))
@@ -297,9 +335,31 @@ int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const v
   if ((rc = check_pack(pack, pack_bytes, bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
   return launch_status(pasa::launch_sparse_attn(q, k, v, pack, idx, selmask, o, (float)scale, (int)bh,
                                                 (int)(seq_len - text_len), (int)text_len, (int)text_valid,
-                                                (int)head_dim, (int)block_size, (int)ns, gamma_literal,
+                                                (int)head_dim, (int)block_size, (int)ns, gamma_literal, rm,
                                                 (hipStream_t)stream),
                        "pasa_sparse_attn");
+}
+
+int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const void* pack, size_t pack_bytes,
+                            const int32_t* idx, const uint32_t* selmask, void* o, double scale, int64_t bh,
+                            int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim,
+                            int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype,
+                            void* stream) {
+  return sparse_attn_packed_impl(q, k, v, pack, pack_bytes, idx, selmask, o, scale, bh, seq_len, text_len,
+                                 text_valid, head_dim, block_size, group_size, ns, gamma_literal, dtype, nullptr,
+                                 stream);
+}
+
+int pasa_sparse_attn_packed_placed(const void* q, const void* k, const void* v, const void* pack,
+                                   size_t pack_bytes, const int32_t* idx, const uint32_t* selmask, void* o,
+                                   double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t text_valid,
+                                   int64_t head_dim, int64_t block_size, int64_t group_size, int64_t ns,
+                                   int gamma_literal, const pasa_placement_t* placement, int dtype, void* stream) {
+  pasa::RowMap rm;
+  int rc;
+  if ((rc = check_placement(placement, bh, seq_len, text_len, head_dim, block_size, &rm))) return rc;
+  return sparse_attn_packed_impl(q, k, v, pack, pack_bytes, idx, selmask, o, scale, bh, seq_len, text_len,
+                                 text_valid, head_dim, block_size, group_size, ns, gamma_literal, dtype, &rm, stream);
 }
 
 int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* kc, const float* vc,

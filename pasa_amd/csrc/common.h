@@ -210,4 +210,39 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- token-major view of a frame-major slice ---------------------------------
+// The HunyuanVideo placement (svg/models/hyvideo/placement.py:73-100): logical row
+// r = p*F + f of the first F*P rows (token p of frame f, token-major) is stored at
+// row f*P + p (frame-major); rows from F*P on (the text tail) are in place.  Heads
+// whose flag is 0 are stored token-major already (identity).
+struct RowMap {
+  int F;                    // frames
+  int P;                    // tokens per frame
+  float invF;               // 1 / F
+  const int32_t* temporal;  // per head; nullptr: every head permuted
+  int heads;                // slice s is head s % heads
+};
+
+// Stored row of logical row r (F*P <= 2^24, so p = r / F is exact up to one step).
+__device__ __forceinline__ int map_row(int r, const RowMap& m) {
+  if (r >= m.F * m.P) return r;
+  int p = (int)((float)r * m.invF);
+  int f = r - p * m.F;
+  if (f < 0) {
+    --p;
+    f += m.F;
+  } else if (f >= m.F) {
+    ++p;
+    f -= m.F;
+  }
+  return f * m.P + p;
+}
+
+// Whether slice bh is permuted (uniform: a scalar load of the head's flag).
+__device__ __forceinline__ bool slice_permuted(const RowMap& m, int bh) {
+  if (m.temporal == nullptr) return true;
+  typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+  return ((const_i32_ptr)m.temporal)[bh % m.heads] != 0;
+}
+
 }  // namespace pasa

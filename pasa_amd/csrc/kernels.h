@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "common.h"
+
 namespace pasa {
 
 constexpr int kMaxSelectBlocks = 4096;  // NT limit of the top-k kernel (LDS-resident row)
@@ -15,9 +17,10 @@ hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* 
                           const int32_t* head_is_temporal, int inverse, hipStream_t stream);
 
 // T: rows of the blocked segment; Tslice: rows per slice (T plus any text rows).
+// rm: nullptr, or the token-major view of frame-major slices (D = 128, BT = 128).
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
-                              int BT, int G, hipStream_t stream);
+                              int BT, int G, const RowMap* rm, hipStream_t stream);
 
 hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,
                          float scale, int use_cov_bias, float* scores, int bh, int NT, int D,
@@ -37,7 +40,7 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
                               int bh, int T, int text, int text_valid, int D, int BT, int NS,
-                              int gamma_literal, hipStream_t stream);
+                              int gamma_literal, const RowMap* rm, hipStream_t stream);
 
 // Dense softmax attention with K4's phase-1 machinery (every key block exact, no
 // selection, no correction), D = 128.  T video rows, then `text` rows of which the

@@ -566,13 +566,15 @@ constexpr int kSchedDsRead = 0x100;
 
 // ALL: dense attention (every key block exact, no selection read, no correction); a
 // separate instantiation so that profiles tell the two launches apart.
-template <int BT, bool ALL>
+// PERM: q, k, v, o are frame-major and the attention runs on their token-major view
+// (rm); every row address goes through map_row.
+template <int BT, bool ALL, bool PERM>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
 void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                         const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
                         const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o,
                         float scale, float c, int T, int NT, int NG, int NW, int xcd_chunk,
-                        int gamma_literal, int text, int text_valid, int n_text_wg, int nbh) {
+                        int gamma_literal, int text, int text_valid, int n_text_wg, int nbh, RowMap rm) {
   constexpr bool all_tiles = ALL;
   using C = K4D<BT>;
   using PK = typename C::PK;
@@ -628,6 +630,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const int Ttot = T + text;
   const int64_t slice = (int64_t)bh * Ttot * D;
   const int qrow = qrow0 + wave * 32 + l32;
+  const bool perm = PERM && slice_permuted(rm, bh);
+  const int qrow_st = perm ? map_row(qrow, rm) : qrow;  // stored row of this lane's query
 
   const uint32_t slice_bytes = (uint32_t)Ttot * D * 2u;
   const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
@@ -635,7 +639,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   bf16x8_t qf[D / 16];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks)
-    qf[ks] = as_bf16x8(buf_load16(qr, ((uint32_t)qrow * D + ks * 16 + h * 8) * 2u));
+    qf[ks] = as_bf16x8(buf_load16(qr, ((uint32_t)qrow_st * D + ks * 16 + h * 8) * 2u));
   // Complete the Q loads now: vector-memory waits the compiler would place at their
   // first use inside the loop would also wait for the tile loads in flight there.
   wait_vmcnt<0>();
@@ -671,7 +675,27 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const uint32_t ks_lds = lds_addr(Ks);
   const uint32_t vs_lds = lds_addr(Vs);
   // A tile is BT key rows starting at row `row0` of the slice (rows past the slice read as zero).
+  // Permuted slices: the lane's rows row0 + 16n + 4(wave + WAVES vw) + lrow are fetched
+  // from their stored rows (computed for K, reused by the V load of the same tile).
+  int st_row[C::VW][BT / 16];
+  auto stored_rows = [&](int row0) {
+#pragma unroll
+    for (int vw = 0; vw < C::VW; ++vw)
+#pragma unroll
+      for (int n = 0; n < BT / 16; ++n)
+        st_row[vw][n] = map_row(row0 + 16 * n + 4 * (wave + C::WAVES * vw) + lrow, rm);
+  };
   auto load_k = [&](int row0) {
+    if (perm) {
+      stored_rows(row0);
+#pragma unroll
+      for (int vw = 0; vw < C::VW; ++vw)
+#pragma unroll
+        for (int n = 0; n < BT / 16; ++n)
+          dma_load16_lds(kd, ks_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256,
+                         (uint32_t)st_row[vw][n] * 256u + (k_lane[vw] & 255u), 0u);
+      return;
+    }
     const uint32_t soff = (uint32_t)row0 * 256u;
 #pragma unroll
     for (int vw = 0; vw < C::VW; ++vw)
@@ -679,7 +703,16 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int n = 0; n < BT / 16; ++n)
         dma_load16_lds(kd, ks_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256, k_lane[vw] + 16 * n * 256, soff);
   };
-  auto load_v = [&](int row0) {
+  auto load_v = [&](int row0) {  // permuted slices: row0 is the tile of the last load_k
+    if (perm) {
+#pragma unroll
+      for (int vw = 0; vw < C::VW; ++vw)
+#pragma unroll
+        for (int n = 0; n < BT / 16; ++n)
+          dma_load16_lds(vd, vs_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256,
+                         (uint32_t)st_row[vw][n] * 256u + (v_lane0 & 255u), 0u);
+      return;
+    }
     const uint32_t soff = (uint32_t)row0 * 256u;
 #pragma unroll
     for (int vw = 0; vw < C::VW; ++vw)
@@ -989,7 +1022,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
 
   const float denom = halves_sum(l_run) + halves_sum(g_run);
   if (qrow < row_limit) {
-    uint16_t* orow = o + slice + (int64_t)qrow * D;
+    uint16_t* orow = o + slice + (int64_t)qrow_st * D;
 #pragma unroll
     for (int et = 0; et < D / 32; ++et)
 #pragma unroll
@@ -1033,7 +1066,7 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
                               int bh, int T, int text, int text_valid, int D, int BT, int NS,
-                              int gamma_literal, hipStream_t stream) {
+                              int gamma_literal, const RowMap* rm, hipStream_t stream) {
   if (text > 0 && D != 128) return hipErrorInvalidValue;  // the text segment is a D = 128 feature
   if (text_valid < 0 || text_valid > text) return hipErrorInvalidValue;
   const int NT = (T + BT - 1) / BT;
@@ -1053,12 +1086,19 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
 #define PASA_K4_LAUNCH(DD, BB)                                                                   \
   hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid_video, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
                      b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
-  if (D == 128 && BT == 128)
-    hipLaunchKernelGGL((k4_sparse_attn_dma<128, false>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
+  if (rm != nullptr) {  // token-major view of frame-major slices: D = 128, BT = 128 only
+    if (D != 128 || BT != 128) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k4_sparse_attn_dma<128, false, true>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b,
+                       cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
+                       n_text_wg, bh, *rm);
+  } else if (D == 128 && BT == 128)
+    hipLaunchKernelGGL((k4_sparse_attn_dma<128, false, false>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b,
+                       cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
+                       n_text_wg, bh, RowMap{});
   else if (D == 128 && BT == 64)
-    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b, cc,
-                       pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid, n_text_wg, bh);
+    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false, false>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b,
+                       cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
+                       n_text_wg, bh, RowMap{});
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
   else if (D == 64 && BT == 64)
@@ -1078,9 +1118,9 @@ hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* 
   const int text_qtiles = (text_valid + BT - 1) / BT + (text - text_valid + BT - 1) / BT;
   const int n_text_wg = (bh * text_qtiles + 7) / 8 * 8;
   dim3 grid(n_text_wg + 8 * bh * xcd_chunk);
-  hipLaunchKernelGGL((k4_sparse_attn_dma<BT, true>), grid, dim3(K4D<BT>::THREADS), 0, stream, (const uint16_t*)q,
-                     (const uint16_t*)k, (const uint16_t*)v, nullptr, nullptr, (uint16_t*)o, scale,
-                     scale * kLog2e, T, NT, 0, 0, xcd_chunk, 1, text, text_valid, n_text_wg, bh);
+  hipLaunchKernelGGL((k4_sparse_attn_dma<BT, true, false>), grid, dim3(K4D<BT>::THREADS), 0, stream,
+                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, nullptr, nullptr, (uint16_t*)o,
+                     scale, scale * kLog2e, T, NT, 0, 0, xcd_chunk, 1, text, text_valid, n_text_wg, bh, RowMap{});
   return hipGetLastError();
 }
 

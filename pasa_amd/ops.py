@@ -17,6 +17,7 @@ tensors must live on a ROCm device and the library must be built.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -64,13 +65,40 @@ class BlockStats:
     hgroup: torch.Tensor
 
 
+@dataclass
+class Placement:
+    """The token-major view of frame-major q, k, v (the HunyuanVideo placement,
+    reference svg/models/hyvideo/placement.py:73-100, :124-153): for heads whose flag
+    is set, logical row p*num_frame + f of the first num_frame*frame_size rows is
+    stored at row f*frame_size + p; the text tail and unflagged heads are in place.
+    ``head_is_temporal``: [H] or [B, H] flags, like the reference's best_mask_idx
+    (None: every head)."""
+    num_frame: int
+    frame_size: int
+    head_is_temporal: Optional[torch.Tensor] = None
+
+    def struct(self, device, batch: int, heads: int):
+        flags = None
+        n = heads
+        if self.head_is_temporal is not None:
+            flags = self.head_is_temporal.to(device=device, dtype=torch.int32).reshape(-1).contiguous()
+            n = flags.numel()
+            if n not in (heads, batch * heads):
+                raise ValueError(f"head_is_temporal has {n} entries for {batch} x {heads} slices")
+        st = _lib.Placement(int(self.num_frame), int(self.frame_size),
+                            None if flags is None else flags.data_ptr(), int(n))
+        return st, flags  # keep flags alive for the call
+
+
 def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int = 64,
-                group_size: int = GROUP_SIZE, text_tokens: int = 0) -> BlockStats:
+                group_size: int = GROUP_SIZE, text_tokens: int = 0,
+                placement: Optional[Placement] = None) -> BlockStats:
     """Block means of Q/K, block sums of V, ||H_j||_F and the group mean of H_j.
 
     Replaces fused_chunk_reduce (reference :268-288; hc is never materialised)
     followed by compute_h_group (:291-301).  With ``text_tokens`` the blocks cover
-    the first T - text_tokens rows only."""
+    the first T - text_tokens rows only.  With ``placement`` the statistics are those
+    of the token-major view of frame-major q, k, v."""
     _check_device(q, k, v)
     B, H, T, D = q.shape
     NT = math.ceil((T - text_tokens) / block_size)
@@ -81,9 +109,13 @@ def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: i
     vc = torch.empty(B, H, NT, D, **f32)
     hnorm = torch.empty(B, H, NT, **f32)
     hgroup = torch.empty(B, H, NG, D, D, **f32)
-    _lib.call("pasa_block_stats", q.data_ptr(), k.data_ptr(), v.data_ptr(), qc.data_ptr(),
-              kc.data_ptr(), vc.data_ptr(), hnorm.data_ptr(), hgroup.data_ptr(), B * H, T, int(text_tokens),
-              D, block_size, group_size, _DTYPES.get(q.dtype, -1), _stream(q))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+            hnorm.data_ptr(), hgroup.data_ptr(), B * H, T, int(text_tokens), D, block_size, group_size)
+    if placement is None:
+        _lib.call("pasa_block_stats", *args, _DTYPES.get(q.dtype, -1), _stream(q))
+    else:
+        st, _keep = placement.struct(q.device, B, H)
+        _lib.call("pasa_block_stats_placed", *args, ctypes.byref(st), _DTYPES.get(q.dtype, -1), _stream(q))
     return BlockStats(qc, kc, vc, hnorm, hgroup)
 
 
@@ -153,34 +185,40 @@ def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_t
 def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: torch.Tensor,
                        sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
                        out: Optional[torch.Tensor] = None, text_tokens: int = 0,
-                       text_valid: Optional[int] = None) -> torch.Tensor:
+                       text_valid: Optional[int] = None, placement: Optional[Placement] = None) -> torch.Tensor:
     """K4 on operands from ``pack_phase2``.  ``text_valid`` (default: all
     ``text_tokens``) is the number of prompt rows at the start of the text segment;
-    the rest are padding (see ``pisa_pg_attention``)."""
+    the rest are padding (see ``pisa_pg_attention``).  ``placement``: q, k, v and the
+    output are frame-major and the attention runs on their token-major view."""
     _check_device(q, k, v, pack)
     if gamma not in ("literal", "consistent"):
         raise ValueError("gamma must be 'literal' or 'consistent'")
     B, H, T, D = q.shape
     o = torch.empty_like(v) if out is None else out
     _check_device(o)
-    _lib.call("pasa_sparse_attn_packed", q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(),
-              pack.numel(), sel.idx.data_ptr(), sel.selmask.data_ptr(), o.data_ptr(), float(scale),
-              B * H, T, int(text_tokens), int(text_tokens if text_valid is None else text_valid), D,
-              block_size, GROUP_SIZE, sel.ns, int(gamma == "literal"),
-              _DTYPES.get(q.dtype, -1), _stream(q))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(), pack.numel(), sel.idx.data_ptr(),
+            sel.selmask.data_ptr(), o.data_ptr(), float(scale), B * H, T, int(text_tokens),
+            int(text_tokens if text_valid is None else text_valid), D, block_size, GROUP_SIZE, sel.ns,
+            int(gamma == "literal"))
+    if placement is None:
+        _lib.call("pasa_sparse_attn_packed", *args, _DTYPES.get(q.dtype, -1), _stream(q))
+    else:
+        st, _keep = placement.struct(q.device, B, H)
+        _lib.call("pasa_sparse_attn_packed_placed", *args, ctypes.byref(st), _DTYPES.get(q.dtype, -1), _stream(q))
     return o
 
 
 def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockStats,
                 sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
                 out: Optional[torch.Tensor] = None, text_tokens: int = 0,
-                text_valid: Optional[int] = None) -> torch.Tensor:
+                text_valid: Optional[int] = None, placement: Optional[Placement] = None) -> torch.Tensor:
     """Exact attention over the selected blocks plus the per-group first-order
     correction of the rest (reference pisa_pg_fwd_kernel :135-262); with
     ``text_tokens``, the prompt keys are exact for every video query block and the
     text rows are dense within their segment."""
     pack = pack_phase2(q, stats, block_size, text_tokens)
-    return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out, text_tokens, text_valid)
+    return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out, text_tokens, text_valid,
+                              placement)
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
@@ -218,6 +256,7 @@ def pisa_pg_attention(
     gamma: str = "literal",
     text_tokens: int = 0,
     text_valid: Optional[int] = None,
+    placement: Optional[Placement] = None,
 ):
     """PISA with per-group first-order correction (drop-in for reference :307-398).
 
@@ -238,13 +277,17 @@ def pisa_pg_attention(
     over cu_seqlens [0, T - text_tokens + text_valid, T], reference
     svg/models/hyvideo/attention.py:314-322).  Video and prompt rows then see the
     video rows and the prompt keys; padding rows see the padding keys.  Default:
-    ``text_tokens`` (no padding)."""
+    ``text_tokens`` (no padding).
+    ``placement``: q, k, v are frame-major (HunyuanVideo's layout) and the operator
+    runs on their token-major view, returning o frame-major; equal to the
+    reference's hunyuan_sparse_head_placement -> attention -> hunyuan_hidden_states_placement
+    (svg/models/hyvideo/attention.py:412-446) in one pass (D = 128, block_size 128)."""
     B, H, T, D = q.shape
     if group_size != GROUP_SIZE:
         raise ValueError(f"the gfx950 kernels use group_size={GROUP_SIZE}")
     scale = D ** -0.5 if scale is None else scale
     NT = math.ceil((T - text_tokens) / block_size)
-    stats = block_stats(q, k, v, block_size, group_size, text_tokens)
+    stats = block_stats(q, k, v, block_size, group_size, text_tokens, placement)
     if use_random and use_cov_bias and noise is None:
         noise = torch.randn(B, H, NT, device=q.device, dtype=torch.float32)
     sel = select_blocks(stats, density, scale, use_cov_bias, noise if use_cov_bias else None)
@@ -252,4 +295,4 @@ def pisa_pg_attention(
         print(f"NT={NT}, N_GROUPS={stats.hgroup.shape[2]}, GROUP_SIZE={group_size}")
         print(f"top_k={sel.ns}, density={density}")
     return sparse_attn(q, k, v, stats, sel, scale, block_size, gamma, text_tokens=text_tokens,
-                       text_valid=text_valid)
+                       text_valid=text_valid, placement=placement)

@@ -246,3 +246,29 @@ def test_dense_attn_validation(lib, kw, code):
     assert lib.pasa_dense_attn(a["q"], a["k"], a["v"], a["o"], a["scale"], a["bh"], a["T"], a["text"], tv, a["D"],
                                a["dtype"], None) == code
     assert lib.pasa_last_error()
+
+
+def test_placed_entries_validation(lib):
+    import ctypes
+    from pasa_amd._lib import Placement
+    bs, sp = lib.pasa_block_stats_placed, lib.pasa_sparse_attn_packed_placed
+    need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 40, 128, 128, 32)
+
+    def stats(pl, D=128, BT=128, T=1000, text=40, bh=2):
+        return bs(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, bh, T, text, D, BT, 32, pl, 0, None)
+
+    def attn(pl, D=128, BT=128, T=1000, text=40, bh=2):
+        return sp(FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, bh, T, text, text, D, BT, 32, 2, 1, pl, 0,
+                  None)
+
+    good = Placement(8, 120, None, 2)                # 8 * 120 = 1000 - 40 video rows
+    for fn in (stats, attn):
+        assert fn(None) == -1
+        assert fn(ctypes.byref(good), D=64) == -3
+        assert fn(ctypes.byref(good), BT=64) == -4
+        assert fn(ctypes.byref(Placement(8, 121, None, 2))) == -2    # F*P != video rows
+        assert fn(ctypes.byref(Placement(0, 120, None, 2))) == -2
+        assert fn(ctypes.byref(Placement(8, 120, None, 3))) == -2    # heads must divide bh
+        big = Placement(2, (1 << 23) + 1, None, 1)                   # F*P > 2^24 rows
+        assert fn(ctypes.byref(big), T=2 * ((1 << 23) + 1), text=0, bh=1) == -6
+        assert lib.pasa_last_error()

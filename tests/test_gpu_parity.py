@@ -414,3 +414,29 @@ def test_processor_dense_split_matches_two_sdpa_calls(device):
                      torch.nn.functional.scaled_dot_product_attention(q[:, :, 421:].float(), k[:, :, 421:].float(),
                                                                        v[:, :, 421:].float())], dim=2).cpu()
     check_parity(o, ref.double(), "processor dense split")
+
+
+# ---------------------------------------------------- placement folded in --
+
+@pytest.mark.parametrize("F,P,text,flags,density", [(5, 200, 0, None, 0.3), (7, 131, 40, [1, 0], 0.25),
+                                                    (3, 300, 256, [0, 1], 0.4), (4, 257, 13, [1, 1], 0.5)])
+def test_placed_attention_equals_permute_attend_unpermute(device, F, P, text, flags, density):
+    """The token-major view of frame-major tensors (placement folded into K2 and K4) is
+    bit-identical to permuting with K1, attending and permuting back."""
+    from pasa_amd import placement as PL
+    H, D = 2, 128
+    T = F * P + text
+    say(f"[placed] F={F} P={P} text={text} flags={flags} density={density}")
+    g = torch.Generator().manual_seed(F * 1000 + P)
+    q, k, v = (torch.randn(1, H, T, D, generator=g).to(torch.bfloat16).to(device) for _ in range(3))
+    fl = None if flags is None else torch.tensor([flags], dtype=torch.int32, device=device)
+    o = ops.pisa_pg_attention(q, k, v, density, block_size=128, text_tokens=text,
+                              placement=ops.Placement(F, P, fl))
+    qs, ks, vs = (torch.empty_like(t) for t in (q, k, v))
+    mask = torch.ones(1, H, dtype=torch.int32, device=device) if fl is None else fl
+    PL.hunyuan_sparse_head_placement(q, k, v, qs, ks, vs, mask, text, F, P)
+    ot = ops.pisa_pg_attention(qs, ks, vs, density, block_size=128, text_tokens=text)
+    ref = torch.empty_like(ot)
+    PL.hunyuan_hidden_states_placement(ot, ref, mask, text, F, P)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)
