@@ -134,6 +134,7 @@ def main() -> int:
     k1f_gbps = 2 * 3 * tensor_bytes / (k1f * 1e-3) / 1e9
     k1i_gbps = 2 * tensor_bytes / (k1i * 1e-3) / 1e9
     k2_bytes = 3 * tensor_bytes + H * NT * (3 * D + 1) * 4 + H * math.ceil(NT / 32) * D * D * 4
+    k3_bytes = 2 * H * NT * D * 4 + H * NT * 4 + H * NT * ns * 4
     log(f"K1 fwd {k1f:.3f} ms ({k1f_gbps:.0f} GB/s)  inv {k1i:.3f} ms ({k1i_gbps:.0f} GB/s)")
 
     # K5: the Wan processor prologue at this shape: projections [1, T, H*D] -> RMSNorm over
@@ -164,11 +165,13 @@ def main() -> int:
     run_placed = lambda: ops.pisa_pg_attention(q, k, v, wl.density, block_size=BT, scale=scale, text_tokens=X,
                                                placement=pl)
 
+    o_frame = torch.empty_like(out)  # `out` keeps the timed call's result for the parity check
+
     def run_separate():
         placement.permute([q, k, v], bufs, F, P, X)
         ot = ops.pisa_pg_attention(bufs[0], bufs[1], bufs[2], wl.density, block_size=BT, scale=scale,
                                    text_tokens=X)
-        placement.permute([ot], [out], F, P, X, inverse=True)
+        placement.permute([ot], [o_frame], F, P, X, inverse=True)
 
     placed_ms = {}
     for name, fn in (("folded", run_placed), ("k1_separate", run_separate)):
@@ -218,6 +221,7 @@ def main() -> int:
         cpu_s = time.perf_counter() - t0
         cpu_tflops = wl.k4_flops(32, ns) * h / H / cpu_s / 1e12
         cpu = {"value": round(cpu_tflops, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+               "os_cpu_count": os.cpu_count(),
                "sample": f"{h} of {H} heads of {args.workload}, one fp32 call of the oracle restatement "
                          f"(oracle/pisa_oracle.py), {cpu_s:.2f} s; ms per full call scaled by H/h = "
                          f"{cpu_s * 1e3 * H / h:.0f}",
@@ -269,6 +273,12 @@ def main() -> int:
                        "inv_ms": round(k1i, 4), "inv_GBps": round(k1i_gbps, 1),
                        "frac_of_hbm_peak_fwd": round(k1f_gbps / PEAK_HBM_GBPS, 4)},
         "k2_GBps_algorithmic": round(k2_bytes / (k2 * 1e-3) / 1e9, 1),
+        "k2_frac_of_hbm_peak": round(k2_bytes / (k2 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        "k3_select": {"us": round(k3 * 1e3, 1), "bytes_algorithmic": k3_bytes,
+                      "GBps": round(k3_bytes / (k3 * 1e-3) / 1e9, 1),
+                      "frac_of_hbm_peak": round(k3_bytes / (k3 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                      "note": "latency-bound: block means in, indices out (2*BH*NT*D*4 + BH*NT*4 + BH*NT*NS*4 B)"},
+        "dense_equivalent_TFLOPs": round(4.0 * D * T * T * H / (ms_per_step * 1e-3) / 1e12, 1),
         "placement_folded": {"ms": round(placed_ms["folded"], 3), "k1_separate_ms": round(placed_ms["k1_separate"], 3),
                              "note": "frame-major q/k/v: placement folded into K2/K4 vs K1 + call + K1 inverse"},
         "dense_attention": {"ms": round(kd_ms, 3), "TFLOPs": round(dense_flops / kd_ms / 1e9, 1),
