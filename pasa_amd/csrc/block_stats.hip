@@ -218,14 +218,14 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 // flight while block j is reduced.  H_j = K^T V reads both MFMA operands with the
 // transposing ds_read_b64_tr_b16 (K^T as A, V as B; the same token order in both).
 // PERM: q, k, v are frame-major; the statistics are those of their token-major view (rm).
-template <bool PERM>
-__global__ __launch_bounds__(256, 1) void k2_block_stats_dma(
+// BT 128 (two 64 KB buffer pairs: one workgroup per CU) or 64 (two per CU).
+template <int BT, bool PERM>
+__global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, float* __restrict__ qc, float* __restrict__ kc,
     float* __restrict__ vc, float* __restrict__ hnorm, float* __restrict__ hgroup, int T, int Tslice,
     int NT, int G, RowMap rm) {
   constexpr int D = 128;
-  constexpr int BT = 128;
   constexpr int TILE = BT * 256;
   __shared__ __attribute__((aligned(1024))) unsigned char Kb[2 * TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char Vb[2 * TILE];
@@ -454,14 +454,14 @@ hipError_t launch_block_stats(const void* q, const void* k, const void* v, float
   auto c = (const uint16_t*)v;
   if (rm != nullptr) {  // token-major view of frame-major slices: D = 128, BT = 128 only
     if (D != 128 || BT != 128) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k2_block_stats_dma<true>, grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm, hgroup,
-                       T, Tslice, NT, G, *rm);
+    hipLaunchKernelGGL((k2_block_stats_dma<128, true>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
+                       hgroup, T, Tslice, NT, G, *rm);
   } else if (D == 128 && BT == 128)
-    hipLaunchKernelGGL(k2_block_stats_dma<false>, grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
+    hipLaunchKernelGGL((k2_block_stats_dma<128, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
                        hgroup, T, Tslice, NT, G, RowMap{});
   else if (D == 128 && BT == 64)
-    hipLaunchKernelGGL((k2_block_stats<128, 64>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
-                       hnorm, hgroup, T, Tslice, NT, G);
+    hipLaunchKernelGGL((k2_block_stats_dma<64, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
+                       hgroup, T, Tslice, NT, G, RowMap{});
   else if (D == 64 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats<64, 128>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
                        hnorm, hgroup, T, Tslice, NT, G);
