@@ -544,7 +544,11 @@ struct K4D {
   static constexpr int VW = 4 / WAVES;                    // 4-row load slots per wave per 16 rows
   static constexpr int TILE_LOADS = TILE / 1024 / WAVES;  // 1 KB direct loads per wave per tile
   using PK = K4DPack<BT>;
-  static constexpr int KBUF = TILE > PK::HT_BYTES ? TILE : PK::HT_BYTES;
+  // BT = 64: Hbar^T goes through the K buffer in two 16 KB halves, so that the
+  // workgroup's LDS fits four two-wave workgroups on a CU.
+  static constexpr int HT_PARTS = BT == 64 ? 2 : 1;
+  static constexpr int HT_PART = PK::HT_BYTES / HT_PARTS;
+  static constexpr int KBUF = TILE > HT_PART ? TILE : HT_PART;
   static constexpr int VBUF = TILE > PK::PART2 ? TILE : PK::PART2;
   static_assert(TILE_LOADS == 8, "load schedule");
 };
@@ -905,8 +909,11 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   };
   // A group's pack is two parts: kbar + V^T (part 2, into Vs) and Hbar^T (into Ks).
   // Part 2 of the next group loads while this group's Hbar^T product runs, and the
-  // next Hbar^T loads while the next group's scores and P.V^ run.
-  constexpr int HT_LOADS = PK::HT_BYTES / 1024 / C::WAVES;
+  // next Hbar^T loads while the next group's scores and P.V^ run.  With HT_PARTS = 2
+  // the second half of Hbar^T (feature rows 64-127) follows the first through Ks.
+  constexpr int HT_PARTS = C::HT_PARTS;
+  constexpr int ETP = (D / 32) / HT_PARTS;  // 32-row output tiles per part
+  constexpr int HT_LOADS = C::HT_PART / 1024 / C::WAVES;
   constexpr int P2_LOADS = PK::PART2 / 1024 / C::WAVES;
   auto load_part2 = [&](int g) {
     const uint32_t gsoff = (uint32_t)(g * PK::BYTES);
@@ -916,8 +923,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       dma_load16_lds(pd, vs_lds + kb * 1024, (uint32_t)(PK::HT_BYTES + kb * 1024 + lane * 16), gsoff);
     }
   };
-  auto load_ht = [&](int g) {
-    const uint32_t gsoff = (uint32_t)(g * PK::BYTES);
+  auto load_ht = [&](int g, int part) {
+    const uint32_t gsoff = (uint32_t)(g * PK::BYTES + part * C::HT_PART);
 #pragma unroll
     for (int n = 0; n < HT_LOADS; ++n) {
       const int kb = n * C::WAVES + wave;  // 1 KB piece of Hbar^T
@@ -927,7 +934,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   int g = next_group(-1);
   if (g >= 0) {  // phase 1 ended with a barrier after the last reads of Ks and Vs
     load_part2(g);
-    load_ht(g);
+    load_ht(g, 0);
   }
   while (g >= 0) {
     const int gn = next_group(g);
@@ -998,25 +1005,33 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       wait_vmcnt<0>();
     barrier_lds_reads_done();
 
-    f32x16_t racc[D / 32];
-#pragma unroll
-    for (int et = 0; et < D / 32; ++et)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) racc[et][r] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-      for (int et = 0; et < D / 32; ++et) {
-        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
-        racc[et] = mfma32(a, qf[ks], racc[et]);
-      }
     const float f = psum * scale;
 #pragma unroll
-    for (int et = 0; et < D / 32; ++et)
+    for (int part = 0; part < HT_PARTS; ++part) {
+      if (part > 0) {  // the next half of this group's Hbar^T (part 2 of gn, issued earlier, lands first)
+        load_ht(g, part);
+        wait_vmcnt<0>();
+        barrier_lds_reads_done();
+      }
+      f32x16_t racc[ETP];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[et][r] = fmaf(racc[et][r], f, oacc[et][r]);
-    barrier_lds_reads_done();  // every wave is done reading Hbar^T of group g
-    if (gn >= 0) load_ht(gn);
+      for (int et = 0; et < ETP; ++et)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) racc[et][r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+        for (int et = 0; et < ETP; ++et) {
+          const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
+          racc[et] = mfma32(a, qf[ks], racc[et]);
+        }
+#pragma unroll
+      for (int et = 0; et < ETP; ++et)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[part * ETP + et][r] = fmaf(racc[et][r], f, oacc[part * ETP + et][r]);
+      barrier_lds_reads_done();  // every wave is done reading this part of Hbar^T
+    }
+    if (gn >= 0) load_ht(gn, 0);
     g = gn;
   }
 
