@@ -9,9 +9,11 @@
 //
 // Stage 1 (k3_scores): a 64x64-tile fp32 GEMM per (slice, tile), VALU FMA with
 //   a fixed d-order, plus the per-key-block log bias.
-// Stage 2 (k3_topk): one wavefront per row sorts 64-bit keys
-//   (orderable(score) << 32 | ~index) with a bitonic network in LDS, emits the
-//   first NS indices and the selection bitmask (one bit per key block).
+// Stage 2 (k3_topk): one wavefront per row finds the NS-th largest score with a
+//   4-pass radix select over the orderable 32-bit score, takes the ties at it by
+//   lowest index, sorts the NS selected 64-bit keys (orderable(score) << 32 | ~index)
+//   with a bitonic network in LDS, and emits the indices and the selection bitmask
+//   (one bit per key block).
 #include "common.h"
 #include "kernels.h"
 
@@ -84,13 +86,6 @@ __global__ __launch_bounds__(256) void k3_scores(const float* __restrict__ qc,
   }
 }
 
-__device__ __forceinline__ uint64_t topk_key(float s, int j) {
-  uint32_t bits = __float_as_uint(s);
-  if ((bits & 0x7fffffffu) == 0) bits = 0;  // -0.0 == +0.0
-  const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - (uint32_t)j);
-}
-
 // Inclusive prefix sum over the 64 lanes of a wavefront.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   const int lane = threadIdx.x & 63;
@@ -102,45 +97,62 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   return x;
 }
 
-// One wavefront per (slice, query block); the row's keys live in registers, KPL per
-// lane (key i*64 + lane).  The NS-th largest key is found exactly by an MSB-first
-// radix select over the 64-bit keys (8 bits per pass; keys are unique because they
-// carry the block index), the NS keys at or above it are compacted into LDS and
-// sorted there in descending order.  Dynamic LDS: NSP * 8 bytes (NSP = pow2 >= NS).
+// Order-preserving map of fp32 scores to uint32 (-0.0 == +0.0).
+__device__ __forceinline__ uint32_t score_ord(float s) {
+  uint32_t bits = __float_as_uint(s);
+  if ((bits & 0x7fffffffu) == 0) bits = 0;
+  return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+
+// One wavefront per row.  The row's ordered scores stay in registers (KPL per lane,
+// index j = 64 i + lane).  An MSB-first radix select over the 32-bit ordered score
+// (4 passes of 8 bits; each pass histograms the keys still matching the prefix, in
+// kCopies LDS copies picked by lane so that equal digits spread their atomics) finds
+// the NS-th largest score T and how many of the scores equal to T are taken; those
+// are the lowest indices (ties go to the lowest index).  The NS selected keys
+// (score << 32 | ~index) are compacted into LDS and sorted descending there with a
+// bitonic network.  Dynamic LDS: NSP * 8 bytes (NSP = pow2 >= NS).
 template <int KPL>
 __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, int NT, int NS, int NSP,
                                               int NW, int32_t* __restrict__ idx,
                                               uint32_t* __restrict__ selmask) {
+  constexpr int kCopies = 8;
   extern __shared__ uint64_t sel[];
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[kCopies][256];
   __shared__ uint32_t words[kMaxSelectBlocks / 32];
   const int row = blockIdx.x;
   const int bh = blockIdx.y;
   const int lane = threadIdx.x;
   const float* srow = scores + ((int64_t)bh * NT + row) * NT;
 
-  uint64_t key[KPL];
+  uint32_t ok[KPL];
 #pragma unroll
   for (int i = 0; i < KPL; ++i) {
     const int j = i * 64 + lane;
-    key[i] = j < NT ? topk_key(srow[j], j) : 0ull;  // 0 is below every real key
+    ok[i] = j < NT ? score_ord(srow[j]) : 0u;
   }
   for (int w = lane; w < NW; w += 64) words[w] = 0u;
 
-  uint64_t prefix = 0ull, mask = 0ull;
-  uint32_t need = (uint32_t)NS;  // rank of the threshold among the keys matching prefix
+  uint32_t prefix = 0u, mask = 0u;
+  uint32_t need = (uint32_t)NS;  // rank of the threshold among the scores matching prefix
+  uint32_t* myhist = hist[lane & (kCopies - 1)];
 #pragma unroll 1
-  for (int shift = 56; shift >= 0; shift -= 8) {
+  for (int shift = 24; shift >= 0; shift -= 8) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) hist[4 * lane + t] = 0u;
+    for (int t = 0; t < 4 * kCopies; ++t) (&hist[0][0])[t * 64 + lane] = 0u;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < KPL; ++i)
-      if (i * 64 + lane < NT && (key[i] & mask) == prefix) atomicAdd(&hist[(uint32_t)(key[i] >> shift) & 255u], 1u);
+      if (i * 64 + lane < NT && (ok[i] & mask) == prefix) atomicAdd(&myhist[(ok[i] >> shift) & 255u], 1u);
     __syncthreads();
     uint32_t hb[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) hb[t] = hist[4 * lane + t];
+    for (int t = 0; t < 4; ++t) {
+      uint32_t x = 0u;
+#pragma unroll
+      for (int cp = 0; cp < kCopies; ++cp) x += hist[cp][4 * lane + t];
+      hb[t] = x;
+    }
     const uint32_t s = hb[0] + hb[1] + hb[2] + hb[3];
     const uint32_t incl = wave_incl_scan(s);
     const uint32_t total = __shfl(incl, 63, 64);
@@ -159,17 +171,29 @@ __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, 
     const int src = __ffsll((long long)hit) - 1;
     const uint32_t bin = (uint32_t)__shfl(found, src, 64);
     need -= (uint32_t)__shfl((int)above, src, 64);
-    prefix |= (uint64_t)bin << shift;
-    mask |= 0xffull << shift;
+    prefix |= bin << shift;
+    mask |= 0xffu << shift;
   }
-  // prefix is now the NS-th largest key: select the keys >= it.
+  // prefix = T, the NS-th largest ordered score; every score above T is selected and,
+  // of the scores equal to T, the `need` with the lowest indices.
+  uint32_t taken = 0u;  // ties at T taken so far (in index order)
   uint32_t cnt = 0u;
+  uint64_t lt = (1ull << lane) - 1ull;
+  bool pick[KPL];
 #pragma unroll
-  for (int i = 0; i < KPL; ++i) cnt += (i * 64 + lane < NT && key[i] >= prefix) ? 1u : 0u;
+  for (int i = 0; i < KPL; ++i) {
+    const bool valid = i * 64 + lane < NT;
+    const bool tie = valid && ok[i] == prefix;
+    const uint64_t tb = __ballot(tie);
+    const uint32_t rank = taken + (uint32_t)__popcll(tb & lt);
+    pick[i] = valid && (ok[i] > prefix || (tie && rank < need));
+    taken += (uint32_t)__popcll(tb);
+    cnt += pick[i] ? 1u : 0u;
+  }
   uint32_t pos = wave_incl_scan(cnt) - cnt;
 #pragma unroll
   for (int i = 0; i < KPL; ++i)
-    if (i * 64 + lane < NT && key[i] >= prefix) sel[pos++] = key[i];
+    if (pick[i]) sel[pos++] = ((uint64_t)ok[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i * 64 + lane));
   for (int i = NS + lane; i < NSP; i += 64) sel[i] = 0ull;
   __syncthreads();
 
