@@ -13,6 +13,7 @@ Prints one JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import math
 import os
@@ -41,6 +42,8 @@ def main() -> int:
     ap.add_argument("--cpu-heads", type=int, default=2, help="heads timed for the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-dit", action="store_true", help="skip the c4 DiT denoising-step sweep")
+    ap.add_argument("--dit-steps", type=int, default=2, help="timed denoising steps per c4 variant")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -201,6 +204,31 @@ def main() -> int:
     log(f"dense attention {kd_ms:.1f} ms ({dense_flops / kd_ms / 1e9:.0f} TFLOP/s); "
         f"PyTorch SDPA {sdpa_ms:.1f} ms ({dense_flops / sdpa_ms / 1e9:.0f} TFLOP/s)")
 
+    # K6 row ops at the Wan-14B row shape (75,600 x 5120): the gated residual + norm2 call,
+    # the heaviest of the block's four (reads x and h, writes h and the normalised row).
+    from pasa_amd import modulate as MOD
+    rows_m, rows_n = 75600, 5120
+    hx = torch.randn(1, rows_m, rows_n, device=dev, dtype=torch.bfloat16)
+    xx = torch.randn(1, rows_m, rows_n, device=dev, dtype=torch.bfloat16)
+    yx = torch.empty_like(hx)
+    gx = torch.randn(1, 1, rows_n, device=dev)
+    wx, bx = torch.randn(rows_n, device=dev, dtype=torch.bfloat16), torch.randn(rows_n, device=dev, dtype=torch.bfloat16)
+    k6_run = lambda: MOD.row_ops(xx, residual=hx, gate=gx, h_out=hx, layernorm=True, weight=wx, bias=bx, y=yx,
+                                 eps=1e-6)
+    k6_run()
+    ka.record()
+    for _ in range(10):
+        k6_run()
+    kb.record()
+    torch.cuda.synchronize()
+    k6_ms = ka.elapsed_time(kb) / 10
+    k6_bytes = 4 * rows_m * rows_n * 2
+    k6_gbps = k6_bytes / (k6_ms * 1e-3) / 1e9
+    log(f"K6 row ops (gated residual + LayerNorm, {rows_m}x{rows_n}) {k6_ms:.3f} ms ({k6_gbps:.0f} GB/s)")
+    del hx, xx, yx, gx, wx, bx
+
+    dit = None if args.no_dit else dit_sweep(torch, dev, args.dit_steps)
+
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
@@ -288,9 +316,92 @@ def main() -> int:
                         "frac_of_hbm_peak": round(k5_gbps / PEAK_HBM_GBPS, 4),
                         "mode": "Wan: RMSNorm over H*D (one rounding) + head split + complex fp64 RoPE, Q/K/V"},
         "parity_vs_oracle": parity,
+        "k6_row_ops": {"ms": round(k6_ms, 4), "GBps": round(k6_gbps, 1), "bytes": k6_bytes,
+                       "frac_of_hbm_peak": round(k6_gbps / PEAK_HBM_GBPS, 4),
+                       "mode": "h = bf16(h + x*gate) in place, y = LayerNorm(h)*w + b, 75600 x 5120 bf16"},
+        "c4_dit_step": dit,
     }
     print(json.dumps(res), flush=True)
     return 0
+
+
+def dit_sweep(torch, dev, steps: int) -> dict:
+    """c4: one denoising step (one transformer forward) of a random-init Wan2.1-1.3B DiT at
+    480p / 81 frames (latent 16x21x60x104 -> 32,760 tokens, 512 random text tokens, bf16),
+    with the stock dense processors (PyTorch SDPA), the PASA processors on their dense
+    warm-up branch, and the PASA processors sparse at each density of the sweep (block 128).
+    ``cos_vs_stock`` compares the step's output with the stock dense step's."""
+    from pasa_amd import wan_dit as W
+    from pasa_amd.processors import replace_wan_attention
+    from pasa_amd.processors import wan as WAN
+
+    cfg = W.WanDiTConfig()
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = W.WanDiT(cfg)
+    model = model.to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(0)
+    latent = W.latent_shape(81, 480, 832)
+    lat = torch.randn(1, *latent, generator=g).to(dev, torch.bfloat16)
+    text = torch.randn(1, 512, cfg.text_dim, generator=g).to(dev, torch.bfloat16)
+    ts = torch.tensor([952], device=dev)
+    tokens = latent[1] * (latent[2] // 2) * (latent[3] // 2)
+
+    def timed():
+        with torch.no_grad():
+            model(lat, ts, text)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                out = model(lat, ts, text)
+            torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps, out.float()
+
+    def cos(a, b):
+        return float(torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0))
+
+    log(f"c4: Wan2.1-1.3B DiT, {cfg.num_layers} blocks, {tokens} tokens; stock dense step")
+    fast_saved = W.WanBlock.fast_kernels
+    W.WanBlock.fast_kernels = False                   # diffusers' PyTorch block forward
+    stock_ms, ref = timed()
+    P = WAN.Wan_PASA_Processor
+    saved = {a: getattr(P, a) for a in ("block_size", "first_times_fp", "rescaled_density")}
+    try:
+        with contextlib.redirect_stdout(sys.stderr):     # the installer prints, as the reference's does
+            replace_wan_attention(W.WanPipelineShape(model), 480, 832, 81, first_layers_fp=0, first_times_fp=0)
+        P.block_size = 128
+        P.first_times_fp, P.rescaled_density = 1000, {952: 0.1}
+        torch_block_ms, _ = timed()                   # PASA sparse at 0.1, PyTorch block elementwise
+        W.WanBlock.fast_kernels = True                # the reference's fast-kernel block (row ops, K6)
+        P.first_times_fp = 0
+        dense_ms, out = timed()                       # timestep 952 > first_times_fp: dense branch
+        res = {"workload": "c4: random-init Wan2.1-1.3B DiT (30 blocks, hidden 1536, 12x128, FFN 8960), "
+                           "latent 16x21x60x104 (32,760 tokens), 512 random text tokens, bf16, timestep 952, "
+                           f"block 128; ms per denoising step, mean of {steps} after one warm-up",
+               "stock_sdpa_ms": round(stock_ms, 2),
+               "note": "stock: SDPA processors and the PyTorch block; PASA rows: PASA processors and the "
+                       "fused block row ops (K6), except sparse_0.1_torch_block_ms",
+               "pasa_dense_branch_ms": round(dense_ms, 2), "pasa_dense_branch_cos_vs_stock": round(cos(out, ref), 6),
+               "sparse_0.1_torch_block_ms": round(torch_block_ms, 2),
+               "sparse": {}}
+        P.first_times_fp = 1000
+        for d in (0.05, 0.1, 0.2, 0.3):
+            P.rescaled_density = {952: d}
+            ms, out = timed()
+            res["sparse"][str(d)] = {"ms": round(ms, 2), "speedup_vs_stock": round(stock_ms / ms, 3),
+                                     "cos_vs_stock": round(cos(out, ref), 6)}
+        log(f"c4: stock {stock_ms:.1f} ms, PASA dense branch {dense_ms:.1f} ms, sparse 0.1 with the PyTorch "
+        f"block {torch_block_ms:.1f} ms, sparse "
+            + ", ".join(f"{d}: {v['ms']:.1f} ms" for d, v in res["sparse"].items()))
+    finally:
+        W.WanBlock.fast_kernels = fast_saved
+        for blk in model.blocks:
+            blk.attn1.set_processor(W.WanAttnProcessor())
+        for a, v in saved.items():
+            setattr(P, a, v)
+    del model, lat, text, ref, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def _cpu_model() -> str:

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 4
+#define PASA_ABI_VERSION 5
 
 typedef enum {
   PASA_OK = 0,
@@ -289,6 +289,40 @@ int pasa_qkv_prologue(const void* xq, const void* xk, const void* xv,
                       int norm, int norm_rounding, double eps,
                       const void* rope_cos, const void* rope_sin, int rope, int64_t rope_rows,
                       int dtype, void* stream);
+
+/* ---- DiT block row operations (K6) ------------------------------------------ */
+
+/* Per token row of `cols` elements (rows = batches * rows_per_batch), in one pass:
+ *   stage A, when residual != NULL:
+ *     h = residual + x * gate   (gate == NULL: h = residual + x), rounded to h_dtype;
+ *     written to h_out when h_out != NULL (h_out may equal residual: in place).
+ *   stage B, when y != NULL, on h (stage A) or on x:
+ *     layernorm != 0:  v = (v - mean) * rstd, mean = sum(v)/cols,
+ *                      rstd = 1/sqrt(sum((v - mean)^2)/cols + eps)
+ *     weight != NULL:  v = v * weight;   bias != NULL: v = v + bias
+ *     scale != NULL:   v = v * (1 + scale) + shift
+ *     written to y as y_dtype.
+ * Every product and sum is one fp32 operation rounded to nearest, as in the
+ * reference's PyTorch fallback; the two row sums are taken per lane in column-chunk
+ * order and then across the 64 lanes of a wave (a fixed order: equal inputs give
+ * equal outputs).  x_dtype, residual_dtype, h_dtype, y_dtype, wb_dtype: bf16 or
+ * fp32; gate, scale, shift: fp32, one row of `cols` per batch, successive rows
+ * `param_stride` elements apart (0: one row for every batch).  cols: a multiple of
+ * 8, at most 8192; every pointer 16-byte aligned, param_stride a multiple of 4.
+ * Buffers among x, residual, h_out and y either do not overlap or are the same
+ * pointer with the same dtype.
+ * Replaces: triton_layernorm_forward (svg/kernels/triton/layernorm.py:9-63,
+ * :110-161, :200-206), triton_modulate_shift_forward (modulate.py:12-78) and
+ * triton_modulate_gate_residual_forward (modulate.py:85-164), as called by the Wan
+ * block (svg/models/wan/custom_models.py:23-115), where one call does a gated
+ * residual and the following LayerNorm and modulation together. */
+int pasa_row_ops(const void* x, int x_dtype,
+                 const void* residual, int residual_dtype, const float* gate, void* h_out, int h_dtype,
+                 int layernorm, const void* weight, const void* bias, int wb_dtype,
+                 const float* scale, const float* shift,
+                 void* y, int y_dtype,
+                 int64_t rows, int64_t cols, int64_t rows_per_batch, int64_t param_stride,
+                 double eps, void* stream);
 
 #ifdef __cplusplus
 }

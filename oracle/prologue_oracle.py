@@ -29,7 +29,14 @@ from __future__ import annotations
 
 from typing import Optional
 
+import numpy as np
 import torch
+
+
+def sqrt_rn(t: torch.Tensor) -> torch.Tensor:
+    """Correctly rounded fp32 square root (numpy's; torch's CPU float32 sqrt is not
+    correctly rounded on every host)."""
+    return torch.from_numpy(np.sqrt(t.detach().cpu().numpy().astype(np.float32)))
 
 
 def _bf16(x: torch.Tensor) -> torch.Tensor:
@@ -40,7 +47,7 @@ def rms_norm_once(x: torch.Tensor, w: Optional[torch.Tensor], eps: float) -> tor
     """RMSNorm over the last dim, one rounding (Triton rmsnorm.py:29-44)."""
     xf = x.float()
     var = (xf * xf).sum(-1, keepdim=True) / xf.shape[-1]
-    rstd = 1.0 / torch.sqrt(var + eps)
+    rstd = 1.0 / sqrt_rn(var + eps)
     y = xf * rstd
     if w is not None:
         y = y * w.float()

@@ -75,9 +75,11 @@ SIGNATURES = {
     "pasa_dense_attn": (_int, [_vp, _vp, _vp, _vp, _dbl, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "pasa_qkv_prologue": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int,
                                  _i64, _i64, _int, _int, _dbl, _vp, _vp, _int, _i64, _int, _vp]),
+    "pasa_row_ops": (_int, [_vp, _int, _vp, _int, _vp, _vp, _int, _int, _vp, _vp, _int, _vp, _vp, _vp, _int,
+                            _i64, _i64, _i64, _i64, _dbl, _vp]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class PasaError(RuntimeError):

@@ -476,4 +476,77 @@ int pasa_qkv_prologue(const void* xq, const void* xk, const void* xv, void* q, v
   return launch_status(pasa::launch_prologue(p, (hipStream_t)stream), "pasa_qkv_prologue");
 }
 
+int pasa_row_ops(const void* x, int x_dtype, const void* residual, int residual_dtype, const float* gate,
+                 void* h_out, int h_dtype,
+                 int layernorm, const void* weight, const void* bias, int wb_dtype, const float* scale,
+                 const float* shift, void* y, int y_dtype, int64_t rows, int64_t cols, int64_t rows_per_batch,
+                 int64_t param_stride, double eps, void* stream) {
+  if (!x) return fail(PASA_ERR_NULL_POINTER, "pasa_row_ops: x is NULL");
+  if (!residual && (gate || h_out))
+    return fail(PASA_ERR_NULL_POINTER, "pasa_row_ops: gate / h_out need a residual");
+  if (!residual && !y) return fail(PASA_ERR_NULL_POINTER, "pasa_row_ops: nothing to compute (residual and y NULL)");
+  if (residual && !h_out && !y) return fail(PASA_ERR_NULL_POINTER, "pasa_row_ops: residual given but no output");
+  if (!y && (layernorm || weight || bias || scale || shift))
+    return fail(PASA_ERR_NULL_POINTER, "pasa_row_ops: stage B arguments given but y is NULL");
+  if ((scale == nullptr) != (shift == nullptr))
+    return fail(PASA_ERR_NULL_POINTER, "pasa_row_ops: scale and shift go together");
+  auto fdt = [](int d) { return d == PASA_DTYPE_BF16 || d == PASA_DTYPE_F32; };
+  if (!fdt(x_dtype) || !fdt(residual_dtype) || !fdt(h_dtype) || !fdt(y_dtype) || !fdt(wb_dtype))
+    return fail(PASA_ERR_DTYPE, "pasa_row_ops: dtypes must be bf16 or fp32");
+  if (rows <= 0 || cols <= 0 || rows_per_batch <= 0 || rows % rows_per_batch != 0)
+    return fail(PASA_ERR_BAD_SHAPE, "pasa_row_ops: rows=%lld, cols=%lld, rows_per_batch=%lld", (long long)rows,
+                (long long)cols, (long long)rows_per_batch);
+  if (cols % 8 != 0 || cols > pasa::row_ops_max_cols())
+    return fail(PASA_ERR_BAD_SHAPE, "pasa_row_ops: cols=%lld must be a multiple of 8 and <= %d", (long long)cols,
+                pasa::row_ops_max_cols());
+  if (param_stride < 0 || param_stride % 4 != 0 || (param_stride > 0 && param_stride < cols))
+    return fail(PASA_ERR_BAD_SHAPE, "pasa_row_ops: param_stride=%lld must be 0 or a multiple of 4 >= cols",
+                (long long)param_stride);
+  if (rows > INT64_MAX / cols / 4 || cdiv(rows, 4) > kMaxI32 ||
+      (param_stride > 0 && rows / rows_per_batch > INT64_MAX / param_stride / 4))
+    return fail(PASA_ERR_OVERFLOW, "pasa_row_ops: sizes overflow");
+  if (layernorm && (!std::isfinite(eps) || eps < 0.0))
+    return fail(PASA_ERR_BAD_ARG, "pasa_row_ops: eps must be finite and >= 0");
+  const void* ptrs[] = {x, residual, gate, h_out, weight, bias, scale, shift, y};
+  for (const void* q : ptrs)
+    if (q && ((uintptr_t)q & 15u))
+      return fail(PASA_ERR_BAD_ARG, "pasa_row_ops: pointers must be 16-byte aligned");
+  // Row buffers: overlapping ones must be the same pointer with the same dtype.
+  struct Buf { const void* p; int dt; };
+  const Buf bufs[4] = {{x, x_dtype}, {residual, residual_dtype}, {h_out, h_dtype}, {y, y_dtype}};
+  for (int i = 0; i < 4; ++i)
+    for (int j = i + 1; j < 4; ++j) {
+      if (!bufs[i].p || !bufs[j].p) continue;
+      const uintptr_t a = (uintptr_t)bufs[i].p, b = (uintptr_t)bufs[j].p;
+      const uintptr_t na = (uintptr_t)(rows * cols * (bufs[i].dt == PASA_DTYPE_F32 ? 4 : 2));
+      const uintptr_t nb = (uintptr_t)(rows * cols * (bufs[j].dt == PASA_DTYPE_F32 ? 4 : 2));
+      const bool overlap = a < b + nb && b < a + na;
+      if (overlap && (a != b || bufs[i].dt != bufs[j].dt))
+        return fail(PASA_ERR_BAD_ARG, "pasa_row_ops: row buffers %d and %d overlap without being the same "
+                    "buffer of the same dtype", i, j);
+    }
+  pasa::RowOpParams p{};
+  p.x = x;
+  p.r = residual;
+  p.gate = gate;
+  p.h = h_out;
+  p.w = weight;
+  p.b = bias;
+  p.scale = scale;
+  p.shift = shift;
+  p.y = y;
+  p.M = rows;
+  p.rows_per_batch = rows_per_batch;
+  p.param_stride = param_stride;
+  p.N = (int)cols;
+  p.x_f32 = x_dtype == PASA_DTYPE_F32;
+  p.r_f32 = residual_dtype == PASA_DTYPE_F32;
+  p.h_f32 = h_dtype == PASA_DTYPE_F32;
+  p.wb_f32 = wb_dtype == PASA_DTYPE_F32;
+  p.y_f32 = y_dtype == PASA_DTYPE_F32;
+  p.ln = layernorm != 0;
+  p.eps = (float)eps;
+  return launch_status(pasa::launch_row_ops(p, (hipStream_t)stream), "pasa_row_ops");
+}
+
 }  // extern "C"

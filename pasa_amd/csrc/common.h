@@ -208,7 +208,51 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// The same butterfly as wave_sum (x += x[lane ^ m], m = 32, 16, ..., 1: each step adds
+// the same pair of partial sums, so the result is bit-identical), with one cross-lane
+// primitive per step instead of an address computation and ds_bpermute: the permlane
+// swaps exchange wave halves / 16-lane rows in the VALU, ds_swizzle's bitmask mode
+// xors the lane id within 32 lanes, and DPP quad_perm xors it within 4.
+__device__ __forceinline__ float wave_sum_xor(float x) {
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), (8 << 10) | 0x1F));
+  x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), (4 << 10) | 0x1F));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));  // xor 2
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));  // xor 1
+  return x;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// One fp32 operation, rounded to nearest even and never fused with a neighbour into an
+// FMA.  hipcc contracts a*b+c by default, and HIP's __fmul_rn / __fadd_rn are plain
+// operators in headers compiled that way; the pragma inside these helpers keeps the
+// steps apart after inlining.  __builtin_sqrtf is the correctly rounded square root
+// (__fsqrt_rn lowers to the approximate v_sqrt_f32 on this toolchain).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+__device__ __forceinline__ float div_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a / b;
+}
+__device__ __forceinline__ float sqrt_rn(float a) { return __builtin_sqrtf(a); }
 
 // ---- token-major view of a frame-major slice ---------------------------------
 // The HunyuanVideo placement (svg/models/hyvideo/placement.py:73-100): logical row

@@ -79,4 +79,27 @@ struct PrologueParams {
 int prologue_max_chunks();  // H * D / 8 limit
 hipError_t launch_prologue(const PrologueParams& p, hipStream_t stream);
 
+// ---- K6: DiT block row operations (modulate.hip) ------------------------------------
+struct RowOpParams {
+  const void* x;              // [M, N] input, bf16 or fp32 (x_f32)
+  const void* r;              // stage A residual [M, N] (bf16 or fp32: r_f32), or null (no stage A)
+  const float* gate;          // stage A gate, fp32 rows of N per batch, or null (plain add)
+  void* h;                    // stage A output [M, N] (bf16 or fp32: h_f32), or null
+  const void* w;              // stage B affine weight [N] (bf16 or fp32: wb_f32), or null
+  const void* b;              // stage B affine bias [N], or null
+  const float* scale;         // stage B modulation, fp32 rows of N per batch, or null
+  const float* shift;         // with scale
+  void* y;                    // stage B output [M, N] (bf16 or fp32: y_f32), or null (no stage B)
+  int64_t M;
+  int64_t rows_per_batch;     // rows sharing one gate/scale/shift row
+  int64_t param_stride;       // elements between the gate/scale/shift rows of successive batches
+  int N;                      // multiple of 8, <= row_ops_max_cols()
+  int x_f32, r_f32, h_f32, wb_f32, y_f32;
+  int ln;                     // LayerNorm in stage B
+  float eps;
+};
+
+int row_ops_max_cols();
+hipError_t launch_row_ops(const RowOpParams& p, hipStream_t stream);
+
 }  // namespace pasa

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void k5_prologue(PrologueParams p, int64_t til
       unpack8(raw[i], f);
       float a = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) a = __fadd_rn(a, __fmul_rn(f[e], f[e]));  // squares rounded, as x*x is
+      for (int e = 0; e < 8; ++e) a = add_rn(a, mul_rn(f[e], f[e]));  // squares rounded, as x*x is
       ss[i] = a;
     }
     if (norm == kNormRow) {
@@ -99,8 +99,8 @@ __global__ __launch_bounds__(256) void k5_prologue(PrologueParams p, int64_t til
       for (int i = 0; i < CPT; ++i) a += ss[i];
 #pragma unroll
       for (int m = 1; m < kLanesPerTok; m <<= 1) a += __shfl_xor(a, m, kLanesPerTok);
-      const float var = a / (float)(p.H * D);
-      const float r = p.round_twice ? rsqrtf(var + p.eps) : 1.0f / sqrtf(var + p.eps);
+      const float var = div_rn(a, (float)(p.H * D));
+      const float r = p.round_twice ? rsqrtf(var + p.eps) : div_rn(1.0f, sqrt_rn(add_rn(var, p.eps)));
 #pragma unroll
       for (int i = 0; i < CPT; ++i) rstd[i] = r;
     } else {  // per head: the head's DC chunks sit on DC consecutive lanes
@@ -108,8 +108,8 @@ __global__ __launch_bounds__(256) void k5_prologue(PrologueParams p, int64_t til
       for (int i = 0; i < CPT; ++i) {
         float a = ss[i];
         for (int m = 1; m < DC; m <<= 1) a += __shfl_xor(a, m, kLanesPerTok);
-        const float var = a / (float)D;
-        rstd[i] = p.round_twice ? rsqrtf(var + p.eps) : 1.0f / sqrtf(var + p.eps);
+        const float var = div_rn(a, (float)D);
+        rstd[i] = p.round_twice ? rsqrtf(var + p.eps) : div_rn(1.0f, sqrt_rn(add_rn(var, p.eps)));
       }
     }
   }
@@ -148,14 +148,14 @@ __global__ __launch_bounds__(256) void k5_prologue(PrologueParams p, int64_t til
       unpack8(*reinterpret_cast<const uint4*>(T.weight + woff), w);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        f[e] = p.round_twice ? bf16r(bf16r(f[e] * rstd[i]) * w[e]) : bf16r((f[e] * rstd[i]) * w[e]);
+        f[e] = p.round_twice ? bf16r(bf16r(f[e] * rstd[i]) * w[e]) : bf16r(mul_rn(mul_rn(f[e], rstd[i]), w[e]));
     }
     if (rope == kRopeCosSinF32) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x0 = f[2 * e], x1 = f[2 * e + 1];
-        f[2 * e] = __fadd_rn(__fmul_rn(x0, cr[2 * e]), __fmul_rn(-x1, sr[2 * e]));
-        f[2 * e + 1] = __fadd_rn(__fmul_rn(x1, cr[2 * e + 1]), __fmul_rn(x0, sr[2 * e + 1]));
+        f[2 * e] = add_rn(mul_rn(x0, cr[2 * e]), mul_rn(-x1, sr[2 * e]));
+        f[2 * e + 1] = add_rn(mul_rn(x1, cr[2 * e + 1]), mul_rn(x0, sr[2 * e + 1]));
       }
     } else if (rope == kRopeComplexF64) {
 #pragma unroll

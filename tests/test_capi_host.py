@@ -272,3 +272,39 @@ def test_placed_entries_validation(lib):
         big = Placement(2, (1 << 23) + 1, None, 1)                   # F*P > 2^24 rows
         assert fn(ctypes.byref(big), T=2 * ((1 << 23) + 1), text=0, bh=1) == -6
         assert lib.pasa_last_error()
+
+
+F16 = 1 << 40            # 16-byte aligned fake device addresses, far apart
+G16 = 2 << 40
+H16 = 3 << 40
+Y16 = 4 << 40
+
+
+def row_ops(lib, **kw):
+    a = dict(x=F16, xdt=0, r=G16, rdt=0, gate=F16 + (1 << 36), h=G16, hdt=0, ln=1, w=None, b=None, wbdt=0,
+             scale=F16 + (2 << 36), shift=F16 + (3 << 36), y=Y16, ydt=0, M=64, N=1536, S=64, ps=0, eps=1e-6)
+    a.update(kw)
+    return lib.pasa_row_ops(a["x"], a["xdt"], a["r"], a["rdt"], a["gate"], a["h"], a["hdt"], a["ln"], a["w"],
+                            a["b"], a["wbdt"], a["scale"], a["shift"], a["y"], a["ydt"], a["M"], a["N"], a["S"],
+                            a["ps"], a["eps"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(x=None), -1),
+    (dict(r=None), -1),                                  # gate / h_out without a residual
+    (dict(r=None, gate=None, h=None, y=None), -1),       # nothing to compute
+    (dict(h=None, y=None), -1),                          # residual without an output
+    (dict(y=None), -1),                                  # stage B arguments without y
+    (dict(shift=None), -1),                              # scale without shift
+    (dict(xdt=1), -7), (dict(ydt=3), -7), (dict(rdt=1), -7), (dict(wbdt=1), -7),
+    (dict(M=0), -2), (dict(N=0), -2), (dict(N=1540), -2), (dict(N=8200), -2), (dict(S=0), -2),
+    (dict(M=65, S=64), -2),                              # rows not a whole number of batches
+    (dict(ps=8), -2), (dict(ps=1538), -2), (dict(ps=-4), -2),
+    (dict(eps=float("nan")), -9), (dict(eps=-1.0), -9),
+    (dict(x=F16 + 8), -9),                               # misaligned
+    (dict(y=G16 + 1024), -9),                            # partial overlap
+    (dict(h=G16, hdt=2), -9),                            # h aliases the residual with another dtype
+])
+def test_row_ops_validation(lib, kw, code):
+    assert row_ops(lib, **kw) == code
+    assert lib.pasa_last_error()
