@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 5
+#define PASA_ABI_VERSION 6
 
 typedef enum {
   PASA_OK = 0,
@@ -113,6 +113,23 @@ int pasa_block_stats(const void* q, const void* k, const void* v,
                      float* qc, float* kc, float* vc, float* hnorm, float* hgroup,
                      int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
                      int64_t block_size, int64_t group_size, int dtype, void* stream);
+
+/* pasa_block_stats with a workspace that lets small grids split each group's blocks
+ * over several workgroups (when BH * NG is small next to the CU count): their partial
+ * sums land in the workspace and a second kernel adds them in a fixed order, so the
+ * result is deterministic (and differs from the unsplit one only in the order of the
+ * group sum).  workspace == NULL: the unsplit kernel; else workspace_bytes must be >=
+ * pasa_block_stats_workspace_bytes(...) (0 when no split would be used) and the
+ * workspace 16-byte aligned.
+ * Replaces: the same reference functions as pasa_block_stats. */
+int pasa_block_stats_ws(const void* q, const void* k, const void* v,
+                        float* qc, float* kc, float* vc, float* hnorm, float* hgroup,
+                        int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
+                        int64_t block_size, int64_t group_size, int dtype,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+size_t pasa_block_stats_workspace_bytes(int64_t bh, int64_t seq_len, int64_t text_len,
+                                        int64_t head_dim, int64_t block_size, int64_t group_size);
 
 /* ---- K3: block scores + deterministic top-k -------------------------------
  * scores[I][j] = sum_d qc[I][d] * (scale * kc[j][d])
@@ -205,7 +222,8 @@ typedef struct {
  * frame-major): the result equals permuting q, k, v to token-major (pasa_permute),
  * running the unplaced entry points and permuting o back, without the three extra
  * passes over HBM.  head_dim 128, block_size 128; arguments otherwise as for the
- * unplaced entry points.
+ * unplaced entry points (pasa_block_stats_placed's workspace as pasa_block_stats_ws's:
+ * with the same workspace the group moments equal the unplaced call's bit for bit).
  * Replaces: hunyuan_sparse_head_placement / hunyuan_hidden_states_placement around the
  * attention call (svg/models/hyvideo/placement.py:124-153, :360-387;
  * svg/models/hyvideo/attention.py:412-446). */
@@ -213,7 +231,8 @@ int pasa_block_stats_placed(const void* q, const void* k, const void* v,
                             float* qc, float* kc, float* vc, float* hnorm, float* hgroup,
                             int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
                             int64_t block_size, int64_t group_size,
-                            const pasa_placement_t* placement, int dtype, void* stream);
+                            const pasa_placement_t* placement, int dtype,
+                            void* workspace, size_t workspace_bytes, void* stream);
 int pasa_sparse_attn_packed_placed(const void* q, const void* k, const void* v, const void* pack,
                                    size_t pack_bytes, const int32_t* idx, const uint32_t* selmask,
                                    void* o, double scale, int64_t bh, int64_t seq_len,

@@ -58,6 +58,9 @@ SIGNATURES = {
                             _vp, _int, _vp]),
     "pasa_block_stats": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _int, _vp]),
+    "pasa_block_stats_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                   _i64, _int, _vp, _sz, _vp]),
+    "pasa_block_stats_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "pasa_select": (_int, [_vp, _vp, _vp, _vp, _dbl, _dbl, _int, _vp, _vp, _vp, _vp, _sz, _i64, _i64,
                            _i64, _vp]),
     "pasa_select_workspace_bytes": (_sz, [_i64, _i64]),
@@ -69,7 +72,7 @@ SIGNATURES = {
     "pasa_sparse_attn_packed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
     "pasa_block_stats_placed": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
-                                       _i64, _pl, _int, _vp]),
+                                       _i64, _pl, _int, _vp, _sz, _vp]),
     "pasa_sparse_attn_packed_placed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                               _i64, _i64, _i64, _i64, _i64, _int, _pl, _int, _vp]),
     "pasa_dense_attn": (_int, [_vp, _vp, _vp, _vp, _dbl, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
@@ -79,7 +82,7 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i64, _dbl, _vp]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class PasaError(RuntimeError):

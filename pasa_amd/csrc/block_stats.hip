@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, float* __restrict__ qc, float* __restrict__ kc,
     float* __restrict__ vc, float* __restrict__ hnorm, float* __restrict__ hgroup, int T, int Tslice,
-    int NT, int G, RowMap rm) {
+    int NT, int G, RowMap rm, int split, float* __restrict__ partials) {
   constexpr int D = 128;
   constexpr int TILE = BT * 256;
   __shared__ __attribute__((aligned(1024))) unsigned char Kb[2 * TILE];
@@ -233,7 +233,9 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   __shared__ float colstat[3 * D];
   __shared__ float red_norm[4];
 
-  const int g = blockIdx.x;
+  // Workgroup (g, part) of a split group takes the part-th of `split` equal runs of its blocks.
+  const int g = blockIdx.x / split;
+  const int part = blockIdx.x - g * split;
   const int bh = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -242,8 +244,10 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   const int l32 = lane & 31;
   const int dq = (wave >> 1) * 64;
   const int eq = (wave & 1) * 64;
-  const int j0 = g * G;
-  const int j1 = min(j0 + G, NT);
+  const int nblk = min(G, NT - g * G);           // blocks in this group
+  const int per = (nblk + split - 1) / split;
+  const int j0 = g * G + min(part * per, nblk);
+  const int j1 = g * G + min((part + 1) * per, nblk);
 
   const int64_t slice = (int64_t)bh * Tslice * D;
   const uint32_t slice_bytes = (uint32_t)T * D * 2u;  // rows >= T read as zero
@@ -427,9 +431,12 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     for (int p = 0; p < BT / 16; ++p) qv[p] = qn[p];
   }
 
+  // Unsplit: the group mean (the reference zero-pads the last group to G blocks).
+  // Split: this part's raw sum, reduced in a fixed order by k2_group_reduce.
   const int NG = (NT + G - 1) / G;
-  float* hg = hgroup + ((int64_t)bh * NG + g) * D * D;
-  const float Gf = (float)G;
+  float* hg = split == 1 ? hgroup + ((int64_t)bh * NG + g) * D * D
+                         : partials + (((int64_t)bh * NG + g) * split + part) * D * D;
+  const float Gf = split == 1 ? (float)G : 1.0f;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -438,30 +445,67 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = dq + mt * 32 + mfma32_row(r, h);
-        hg[d * D + e] = gacc[mt][nt][r] / Gf;
+        hg[d * D + e] = split == 1 ? gacc[mt][nt][r] / Gf : gacc[mt][nt][r];
       }
     }
 }
 
+// hgroup[bh, g] = (sum over parts p = 0..split-1 of partials[bh, g, p]) / G, summed in
+// part order (deterministic).  One float4 of one group per thread; 256 threads cover a
+// 1024-element slab of the group's D*D matrix, so a launch has NG * bh * D*D/1024
+// workgroups (1536 at the Wan-1.3B shape) rather than one per group.
+__global__ __launch_bounds__(256) void k2_group_reduce(const float* __restrict__ partials,
+                                                       float* __restrict__ hgroup, int split, int G, int dd,
+                                                       int64_t groups) {
+  const int slabs = dd / 1024;
+  const int64_t grp = blockIdx.x / slabs;
+  if (grp >= groups) return;
+  const int i = (int)(blockIdx.x - grp * slabs) * 256 + threadIdx.x;  // float4 index within the group
+  const int n4 = dd / 4;
+  const float4* src = reinterpret_cast<const float4*>(partials + grp * split * (int64_t)dd);
+  float4 a = src[i];
+  for (int p = 1; p < split; ++p) {
+    const float4 b = src[(int64_t)p * n4 + i];
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  }
+  const float Gf = (float)G;
+  reinterpret_cast<float4*>(hgroup + grp * (int64_t)dd)[i] = make_float4(a.x / Gf, a.y / Gf, a.z / Gf, a.w / Gf);
+}
+
+// Parts per group: enough workgroups for about two per CU (256 CUs) when the grid of
+// groups alone is small, at least 4 blocks per part.  Only the D = 128 direct-to-LDS
+// kernels split.
+int block_stats_split(int bh, int T, int D, int BT, int G) {
+  if (D != 128 || (BT != 128 && BT != 64)) return 1;
+  const int NT = (T + BT - 1) / BT;
+  const int64_t groups = (int64_t)((NT + G - 1) / G) * bh;
+  const int nblk = min(G, NT);
+  int split = 1;
+  while (split < 8 && groups * split < 512 && nblk / (2 * split) >= 4) split *= 2;
+  return split;
+}
+
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
-                              int BT, int G, const RowMap* rm, hipStream_t stream) {
+                              int BT, int G, const RowMap* rm, float* partials, int split, hipStream_t stream) {
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + G - 1) / G;
-  dim3 grid(NG, bh);
+  if (split < 1 || split > G || (split > 1 && (partials == nullptr || D != 128 || (BT != 128 && BT != 64))))
+    return hipErrorInvalidValue;
+  dim3 grid(NG * split, bh);
   auto a = (const uint16_t*)q;
   auto b = (const uint16_t*)k;
   auto c = (const uint16_t*)v;
   if (rm != nullptr) {  // token-major view of frame-major slices: D = 128, BT = 128 only
     if (D != 128 || BT != 128) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k2_block_stats_dma<128, true>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, *rm);
+                       hgroup, T, Tslice, NT, G, *rm, split, partials);
   } else if (D == 128 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats_dma<128, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, RowMap{});
+                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials);
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k2_block_stats_dma<64, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, RowMap{});
+                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials);
   else if (D == 64 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats<64, 128>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
                        hnorm, hgroup, T, Tslice, NT, G);
@@ -470,6 +514,13 @@ hipError_t launch_block_stats(const void* q, const void* k, const void* v, float
                        hnorm, hgroup, T, Tslice, NT, G);
   else
     return hipErrorInvalidValue;
+  if (split > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t groups = (int64_t)NG * bh;  // D = 128: D*D / 1024 = 16 slabs per group
+    hipLaunchKernelGGL(k2_group_reduce, dim3((unsigned)(groups * (D * D / 1024))), dim3(256), 0, stream,
+                       (const float*)partials, hgroup, split, G, D * D, groups);
+  }
   return hipGetLastError();
 }
 

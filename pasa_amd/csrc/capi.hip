@@ -155,7 +155,7 @@ int pasa_permute(const void* src0, const void* src1, const void* src2, void* dst
 static int block_stats_impl(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
                             float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t head_dim, int64_t block_size, int64_t group_size, int dtype,
-                            const pasa::RowMap* rm, void* stream) {
+                            const pasa::RowMap* rm, void* workspace, size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
   if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_block_stats: only bf16 inputs are supported");
   int rc;
@@ -165,17 +165,49 @@ static int block_stats_impl(const void* q, const void* k, const void* v, float* 
   if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
   if ((rc = check_text(seq_len, text_len, head_dim))) return rc;
   if (group_size <= 0 || group_size > 1 << 20) return fail(PASA_ERR_GROUP_SIZE, "group_size %lld must be in [1, 2^20]", (long long)group_size);
+  int split = 1;
+  if (workspace != nullptr) {
+    split = pasa::block_stats_split((int)bh, (int)(seq_len - text_len), (int)head_dim, (int)block_size,
+                                    (int)group_size);
+    const size_t need = pasa_block_stats_workspace_bytes(bh, seq_len, text_len, head_dim, block_size, group_size);
+    if (workspace_bytes < need)
+      return fail(PASA_ERR_WORKSPACE, "pasa_block_stats_ws: workspace %zu bytes < %zu", workspace_bytes, need);
+    if (((uintptr_t)workspace | (uintptr_t)hgroup) & 15u)
+      return fail(PASA_ERR_BAD_ARG, "pasa_block_stats_ws: workspace and hgroup must be 16-byte aligned");
+  }
   return launch_status(pasa::launch_block_stats(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh,
                                                 (int)(seq_len - text_len), (int)seq_len, (int)head_dim,
-                                                (int)block_size, (int)group_size, rm, (hipStream_t)stream),
+                                                (int)block_size, (int)group_size, rm, (float*)workspace, split,
+                                                (hipStream_t)stream),
                        "pasa_block_stats");
+}
+
+size_t pasa_block_stats_workspace_bytes(int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
+                                        int64_t block_size, int64_t group_size) {
+  if (bh <= 0 || bh > kMaxGridY || seq_len <= 0 || seq_len > kMaxI32 / 2 || text_len < 0 || text_len >= seq_len ||
+      (head_dim != 64 && head_dim != 128) || (block_size != 64 && block_size != 128) || group_size <= 0 ||
+      group_size > 1 << 20)
+    return 0;
+  const int split = pasa::block_stats_split((int)bh, (int)(seq_len - text_len), (int)head_dim, (int)block_size,
+                                            (int)group_size);
+  if (split == 1) return 0;
+  const int64_t ng = cdiv(cdiv(seq_len - text_len, block_size), group_size);
+  return (size_t)bh * (size_t)ng * (size_t)split * (size_t)(head_dim * head_dim) * sizeof(float);
 }
 
 int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
                      float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
                      int64_t head_dim, int64_t block_size, int64_t group_size, int dtype, void* stream) {
   return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
-                          group_size, dtype, nullptr, stream);
+                          group_size, dtype, nullptr, nullptr, 0, stream);
+}
+
+int pasa_block_stats_ws(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
+                        float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
+                        int64_t head_dim, int64_t block_size, int64_t group_size, int dtype, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
+                          group_size, dtype, nullptr, workspace, workspace_bytes, stream);
 }
 
 // The placement's row map, after checking it fits the slices it will address.
@@ -200,12 +232,13 @@ static int check_placement(const pasa_placement_t* pl, int64_t bh, int64_t seq_l
 int pasa_block_stats_placed(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
                             float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t head_dim, int64_t block_size, int64_t group_size,
-                            const pasa_placement_t* placement, int dtype, void* stream) {
+                            const pasa_placement_t* placement, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   pasa::RowMap rm;
   int rc;
   if ((rc = check_placement(placement, bh, seq_len, text_len, head_dim, block_size, &rm))) return rc;
   return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
-                          group_size, dtype, &rm, stream);
+                          group_size, dtype, &rm, workspace, workspace_bytes, stream);
 }
 
 size_t pasa_select_workspace_bytes(int64_t bh, int64_t num_blocks) {

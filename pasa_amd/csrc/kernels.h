@@ -18,9 +18,12 @@ hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* 
 
 // T: rows of the blocked segment; Tslice: rows per slice (T plus any text rows).
 // rm: nullptr, or the token-major view of frame-major slices (D = 128, BT = 128).
+// split > 1: each group's blocks go to `split` workgroups, whose raw partial sums
+// (partials: [bh, NG, split, D, D] fp32) a second kernel reduces in order into hgroup.
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
-                              int BT, int G, const RowMap* rm, hipStream_t stream);
+                              int BT, int G, const RowMap* rm, float* partials, int split, hipStream_t stream);
+int block_stats_split(int bh, int T, int D, int BT, int G);  // the split the launcher is given by the C ABI
 
 hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,
                          float scale, int use_cov_bias, float* scores, int bh, int NT, int D,

@@ -92,13 +92,15 @@ class Placement:
 
 def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int = 64,
                 group_size: int = GROUP_SIZE, text_tokens: int = 0,
-                placement: Optional[Placement] = None) -> BlockStats:
+                placement: Optional[Placement] = None, split: bool = True) -> BlockStats:
     """Block means of Q/K, block sums of V, ||H_j||_F and the group mean of H_j.
 
     Replaces fused_chunk_reduce (reference :268-288; hc is never materialised)
     followed by compute_h_group (:291-301).  With ``text_tokens`` the blocks cover
     the first T - text_tokens rows only.  With ``placement`` the statistics are those
-    of the token-major view of frame-major q, k, v."""
+    of the token-major view of frame-major q, k, v.  ``split`` lets small grids (few
+    heads x groups) spread each group over several workgroups (``pasa_block_stats_ws``;
+    deterministic, the group sum in a different fixed order)."""
     _check_device(q, k, v)
     B, H, T, D = q.shape
     NT = math.ceil((T - text_tokens) / block_size)
@@ -111,11 +113,18 @@ def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: i
     hgroup = torch.empty(B, H, NG, D, D, **f32)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
             hnorm.data_ptr(), hgroup.data_ptr(), B * H, T, int(text_tokens), D, block_size, group_size)
-    if placement is None:
+    ws_bytes = _lib.load().pasa_block_stats_workspace_bytes(B * H, T, int(text_tokens), D, block_size,
+                                                            group_size) if split else 0
+    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes > 0 else None
+    ws_ptr = None if ws is None else ws.data_ptr()
+    if placement is None and ws is not None:
+        _lib.call("pasa_block_stats_ws", *args, _DTYPES.get(q.dtype, -1), ws_ptr, ws_bytes, _stream(q))
+    elif placement is None:
         _lib.call("pasa_block_stats", *args, _DTYPES.get(q.dtype, -1), _stream(q))
     else:
         st, _keep = placement.struct(q.device, B, H)
-        _lib.call("pasa_block_stats_placed", *args, ctypes.byref(st), _DTYPES.get(q.dtype, -1), _stream(q))
+        _lib.call("pasa_block_stats_placed", *args, ctypes.byref(st), _DTYPES.get(q.dtype, -1), ws_ptr,
+                  ws_bytes, _stream(q))
     return BlockStats(qc, kc, vc, hnorm, hgroup)
 
 

@@ -255,7 +255,7 @@ def test_placed_entries_validation(lib):
     need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 40, 128, 128, 32)
 
     def stats(pl, D=128, BT=128, T=1000, text=40, bh=2):
-        return bs(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, bh, T, text, D, BT, 32, pl, 0, None)
+        return bs(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, bh, T, text, D, BT, 32, pl, 0, None, 0, None)
 
     def attn(pl, D=128, BT=128, T=1000, text=40, bh=2):
         return sp(FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, bh, T, text, text, D, BT, 32, 2, 1, pl, 0,
@@ -308,3 +308,18 @@ def row_ops(lib, **kw):
 def test_row_ops_validation(lib, kw, code):
     assert row_ops(lib, **kw) == code
     assert lib.pasa_last_error()
+
+
+def test_block_stats_workspace(lib):
+    # the c2 grid (40 slices x 19 groups) needs no split; c1's (12 x 8) splits 8 ways
+    assert lib.pasa_block_stats_workspace_bytes(40, 75600, 0, 128, 128, 32) == 0
+    assert lib.pasa_block_stats_workspace_bytes(12, 32760, 0, 128, 128, 32) == 12 * 8 * 8 * 128 * 128 * 4
+    assert lib.pasa_block_stats_workspace_bytes(12, 32760, 0, 64, 128, 32) == 0       # D = 64 kernels do not split
+    assert lib.pasa_block_stats_workspace_bytes(0, 32760, 0, 128, 128, 32) == 0
+    need = lib.pasa_block_stats_workspace_bytes(12, 32760, 0, 128, 128, 32)
+    args = [FAKE] * 8 + [12, 32760, 0, 128, 128, 32, 0]
+    assert lib.pasa_block_stats_ws(*args, F16, need - 1, None) == -8                  # too small
+    assert b"workspace" in lib.pasa_last_error()
+    assert lib.pasa_block_stats_ws(*args, F16 + 4, need, None) == -9                  # misaligned
+    a2 = [FAKE] * 7 + [None] + [12, 32760, 0, 128, 128, 32, 0]
+    assert lib.pasa_block_stats_ws(*a2, F16, need, None) == -1                        # hgroup NULL

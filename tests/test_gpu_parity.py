@@ -154,6 +154,28 @@ def test_block_stats(device, heads, grid, D, BT):
     close(st.hgroup, hg, "hgroup", 1e-4)
 
 
+@pytest.mark.parametrize("heads,T,BT", [(12, 32760, 128), (2, 5000, 128), (3, 9000, 64), (1, 1100, 128)])
+def test_block_stats_split_matches_unsplit(device, heads, T, BT):
+    """Small grids split each group over several workgroups: the per-block statistics
+    are the same computation (bit-identical), the group moment differs only in the order
+    of its sum.  (2, 5000, 128) ends in a partial group of 8 blocks."""
+    from pasa_amd import _lib
+    need = _lib.load().pasa_block_stats_workspace_bytes(heads, T, 0, 128, BT, 32)
+    assert need > 0, "shape chosen to split"
+    g = torch.Generator().manual_seed(T)
+    q, k, v = (torch.randn(1, heads, T, 128, generator=g).to(device, torch.bfloat16) for _ in range(3))
+    say(f"[K2 split] heads={heads} T={T} BT={BT} workspace={need >> 20} MiB")
+    a = ops.block_stats(q, k, v, BT, 32, split=True)
+    b = ops.block_stats(q, k, v, BT, 32, split=False)
+    for name in ("qc", "kc", "vc", "hnorm"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    d = float((a.hgroup - b.hgroup).abs().max())
+    scale = float(b.hgroup.abs().max())
+    say(f"[K2 split]   hgroup max |split - unsplit| {d:.3e} of max {scale:.3e}")
+    assert d <= 1e-5 * scale
+    assert torch.equal(a.hgroup, ops.block_stats(q, k, v, BT, 32, split=True).hgroup)   # deterministic
+
+
 # ---------------------------------------------------------------- K3 --------
 
 @pytest.mark.parametrize("NT,ns", [(16, 4), (100, 15), (591, 59), (929, 92), (1024, 1), (4096, 409), (3, 3)])
