@@ -43,6 +43,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-dit", action="store_true", help="skip the c4 DiT denoising-step sweep")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the c1 / c3 / c2-at-block-64 step timings")
     ap.add_argument("--dit-steps", type=int, default=2, help="timed denoising steps per c4 variant")
     args = ap.parse_args()
 
@@ -227,6 +229,17 @@ def main() -> int:
     log(f"K6 row ops (gated residual + LayerNorm, {rows_m}x{rows_n}) {k6_ms:.3f} ms ({k6_gbps:.0f} GB/s)")
     del hx, xx, yx, gx, wx, bx
 
+    others = None
+    if not args.no_other_configs and args.workload == "c2":
+        del bufs
+        import dataclasses
+        others = {}
+        for name, w in (("c1", WORKLOADS["c1"]), ("c3", WORKLOADS["c3"]),
+                        ("c2_block64", dataclasses.replace(wl, block_size=64))):
+            others[name] = config_step(torch, ops, make_inputs, w, dev, args.seed)
+            log(f"{name}: {others[name]['ms_per_step']:.3f} ms/step, {others[name]['TFLOPs_effective']:.1f} "
+                f"TFLOP/s effective, K4 {others[name]['k4_ms']:.3f} ms")
+
     dit = None if args.no_dit else dit_sweep(torch, dev, args.dit_steps)
 
     traffic = None
@@ -319,10 +332,49 @@ def main() -> int:
         "k6_row_ops": {"ms": round(k6_ms, 4), "GBps": round(k6_gbps, 1), "bytes": k6_bytes,
                        "frac_of_hbm_peak": round(k6_gbps / PEAK_HBM_GBPS, 4),
                        "mode": "h = bf16(h + x*gate) in place, y = LayerNorm(h)*w + b, 75600 x 5120 bf16"},
+        "other_configs": others,
         "c4_dit_step": dit,
     }
     print(json.dumps(res), flush=True)
     return 0
+
+
+def config_step(torch, ops, make_inputs, wl, dev, seed: int, steps: int = 10, warmup: int = 3) -> dict:
+    """ms per PISA-PG call (K2 + pack + K3 + K4, inputs resident) of another workload,
+    with its K4 time and the effective rate F / t of its algorithmic K4 FLOPs."""
+    q, k, v = (t.to(dev) for t in make_inputs(wl, seed=seed))
+    BT, X = wl.block_size, wl.text_tokens
+    ns = ops.num_selected(wl.density, wl.num_blocks())
+    flops = wl.k4_flops(32, ns)
+    out = torch.empty_like(v)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+
+    def call(e=None):
+        st = ops.block_stats(q, k, v, BT, 32, text_tokens=X)
+        pack = ops.pack_phase2(q, st, BT, X)
+        sel = ops.select_blocks(st, wl.density, wl.op_scale)
+        if e is not None:
+            e[0].record()
+        ops.sparse_attn_packed(q, k, v, pack, sel, wl.op_scale, BT, out=out, text_tokens=X)
+        if e is not None:
+            e[1].record()
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        call(ev[i])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    k4 = statistics.mean(e[0].elapsed_time(e[1]) for e in ev)
+    res = {"workload": f"{wl.name}: H={wl.heads} T={wl.seq_len} D={wl.head_dim} block {BT} density {wl.density} "
+                       f"NS={ns}" + (f" text {X}" if X else ""),
+           "ms_per_step": round(ms, 4), "k4_ms": round(k4, 4), "k4_TFLOPs": round(flops / k4 / 1e9, 1),
+           "TFLOPs_effective": round(flops / ms / 1e9, 1), "flops": flops}
+    del q, k, v, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def dit_sweep(torch, dev, steps: int) -> dict:
