@@ -7,8 +7,8 @@
 // is defined against fp32 math).  torch.topk leaves the order of equal scores
 // unspecified; this kernel fixes it: (score desc, index asc), -0.0 == +0.0.
 //
-// Stage 1 (k3_scores): a 64x64-tile fp32 GEMM per (slice, tile), VALU FMA with
-//   a fixed d-order, plus the per-key-block log bias.
+// Stage 1 (k3_scores): a 64x64-tile fp32 GEMM per (slice, tile) on the fp32 MFMA,
+//   with a fixed d-order, plus the per-key-block log bias.
 // Stage 2 (k3_topk): one wavefront per row finds the NS-th largest score with a
 //   4-pass radix select over the orderable 32-bit score, takes the ties at it by
 //   lowest index, sorts the NS selected 64-bit keys (orderable(score) << 32 | ~index)
@@ -20,69 +20,77 @@
 namespace pasa {
 
 constexpr int kScoreTile = 64;
-constexpr int kScoreKC = 32;
 
+// One workgroup per 64 x 64 tile of one slice's score matrix, one 32 x 32 sub-tile per
+// wave, on the fp32 MFMA (v_mfma_f32_32x32x2_f32: twice the rate of scalar fp32 FMAs).
+// The dot product over d is taken in a fixed permuted order: in step s the lanes of
+// half-wave hh supply d = hh * D/2 + s, so a lane walks contiguous d and one 16-byte LDS
+// read feeds four MFMAs.  Rows are staged in LDS as fp32 with a 4-float pad; kc * scale is
+// rounded to fp32 before the product, as the reference computes it.
+template <int D>
 __global__ __launch_bounds__(256) void k3_scores(const float* __restrict__ qc,
                                                  const float* __restrict__ kc,
                                                  const float* __restrict__ hnorm,
                                                  const float* __restrict__ noise, float scale,
-                                                 int use_cov_bias, float* __restrict__ scores,
-                                                 int NT, int D) {
-  __shared__ float As[kScoreTile][kScoreKC + 1];
-  __shared__ float Bs[kScoreTile][kScoreKC + 1];
+                                                 int use_cov_bias, float* __restrict__ scores, int NT) {
+  constexpr int RS = D + 4;  // padded row stride (floats)
+  __shared__ __attribute__((aligned(16))) float As[kScoreTile * RS];
+  __shared__ __attribute__((aligned(16))) float Bs[kScoreTile * RS];
   const int bh = blockIdx.z;
   const int i0 = blockIdx.y * kScoreTile;
   const int j0 = blockIdx.x * kScoreTile;
   const int tid = threadIdx.x;
-  const int tx = tid & 15;
-  const int ty = tid >> 4;
   const float* qb = qc + (int64_t)bh * NT * D;
   const float* kb = kc + (int64_t)bh * NT * D;
-
-  float acc[4][4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = 0.f;
-
-  for (int d0 = 0; d0 < D; d0 += kScoreKC) {
-    __syncthreads();
-    for (int u = tid; u < kScoreTile * kScoreKC; u += 256) {
-      const int r = u / kScoreKC;
-      const int c = u - r * kScoreKC;
-      const int gi = i0 + r;
-      const int gj = j0 + r;
-      As[r][c] = gi < NT ? qb[(int64_t)gi * D + d0 + c] : 0.f;
-      Bs[r][c] = gj < NT ? scale * kb[(int64_t)gj * D + d0 + c] : 0.f;  // kc * scale first
+  // Stage 64 rows of qc and of scale * kc, 16 bytes per thread per step.
+  constexpr int C4 = D / 4;  // float4 per row
+  for (int u = tid; u < kScoreTile * C4; u += 256) {
+    const int r = u / C4;
+    const int c4 = u - r * C4;
+    const int gi = i0 + r;
+    const int gj = j0 + r;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (gi < NT) a = *reinterpret_cast<const float4*>(qb + (int64_t)gi * D + 4 * c4);
+    if (gj < NT) {
+      b = *reinterpret_cast<const float4*>(kb + (int64_t)gj * D + 4 * c4);
+      b = make_float4(scale * b.x, scale * b.y, scale * b.z, scale * b.w);  // kc * scale first
     }
-    __syncthreads();
-#pragma unroll 8
-    for (int c = 0; c < kScoreKC; ++c) {
-      float av[4], bv[4];
+    *reinterpret_cast<float4*>(As + r * RS + 4 * c4) = a;
+    *reinterpret_cast<float4*>(Bs + r * RS + 4 * c4) = b;
+  }
+  __syncthreads();
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+  const int ar = (wave >> 1) * 32 + l32;  // row of A (query block) this lane supplies
+  const int br = (wave & 1) * 32 + l32;   // row of B (key block)
+  const float* ap = As + ar * RS + hh * (D / 2);
+  const float* bp = Bs + br * RS + hh * (D / 2);
+  f32x16_t acc;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) av[a] = As[ty + 16 * a][c];
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) bv[b] = Bs[tx + 16 * b][c];
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = fmaf(av[a], bv[b], acc[a][b]);
-    }
+  for (int s4 = 0; s4 < D / 8; ++s4) {
+    const float4 a = *reinterpret_cast<const float4*>(ap + 4 * s4);
+    const float4 b = *reinterpret_cast<const float4*>(bp + 4 * s4);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+  }
+  // C: row (query block) 8(r>>2) + 4hh + (r&3) of the wave's sub-tile, column (key block) l32.
+  const int gj = j0 + (wave & 1) * 32 + l32;
+  if (gj >= NT) return;
+  float bias = 0.f;
+  if (use_cov_bias) {
+    bias = logf(hnorm[(int64_t)bh * NT + gj] + 1e-6f);
+    if (noise) bias = bias + noise[(int64_t)bh * NT + gj];
   }
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int gj = j0 + tx + 16 * b;
-    if (gj >= NT) continue;
-    float bias = 0.f;
-    if (use_cov_bias) {
-      bias = logf(hnorm[(int64_t)bh * NT + gj] + 1e-6f);
-      if (noise) bias = bias + noise[(int64_t)bh * NT + gj];
-    }
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int gi = i0 + ty + 16 * a;
-      if (gi < NT) scores[((int64_t)bh * NT + gi) * NT + gj] = acc[a][b] + bias;
-    }
+  for (int r = 0; r < 16; ++r) {
+    const int gi = i0 + (wave >> 1) * 32 + mfma32_row(r, hh);
+    if (gi < NT) scores[((int64_t)bh * NT + gi) * NT + gj] = acc[r] + bias;
   }
 }
 
@@ -229,8 +237,14 @@ hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, c
                          float scale, int use_cov_bias, float* scores, int bh, int NT, int D,
                          hipStream_t stream) {
   dim3 grid((NT + kScoreTile - 1) / kScoreTile, (NT + kScoreTile - 1) / kScoreTile, bh);
-  hipLaunchKernelGGL(k3_scores, grid, dim3(256), 0, stream, qc, kc, hnorm, noise, scale,
-                     use_cov_bias, scores, NT, D);
+  if (D == 128)
+    hipLaunchKernelGGL(k3_scores<128>, grid, dim3(256), 0, stream, qc, kc, hnorm, noise, scale, use_cov_bias,
+                       scores, NT);
+  else if (D == 64)
+    hipLaunchKernelGGL(k3_scores<64>, grid, dim3(256), 0, stream, qc, kc, hnorm, noise, scale, use_cov_bias,
+                       scores, NT);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
