@@ -87,10 +87,15 @@ __device__ __forceinline__ void buf_load16_lds(rsrc_t r, unsigned char* lds_base
 // rsrc: buffer descriptor words; lds_addr: LDS byte address (wave-uniform).
 __device__ __forceinline__ void dma_load16_lds(u32x4_t rsrc, uint32_t lds_addr, uint32_t byte_off,
                                                uint32_t soff) {
-  // m0 is set here on every use; kernels calling this issue no compiler-generated
-  // LDS-direct loads, so nothing else relies on m0 across it.
+  // m0 is set here on every use; it is a reserved register (the compiler keeps no
+  // value in it across this statement), and the kernels calling this issue no
+  // compiler-generated LDS-direct loads.  An LDS-direct load that reads m0 right
+  // after an SALU write of it needs one wait state on gfx9-family chips (the compiler
+  // pads its own such pairs with s_nop 0, but cannot see inside inline assembly):
+  // without it the load may take the previous m0 and write its data over the
+  // previous load's LDS destination when the wave issues unimpeded.
   // lds_addr and soff must be wave-uniform; readfirstlane puts them in SGPRs.
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(byte_off), "s"(rsrc),
                  "s"(__builtin_amdgcn_readfirstlane(soff))
