@@ -25,15 +25,22 @@
 // bitmask) instead of top-k order: exact online softmax is order-independent up
 // to rounding, and the ascending sweep keeps the workgroups of one XCD on
 // nearby key blocks at the same time, so the K/V tiles they share hit in L2.
-// The running max used for exponentiation is updated lazily (only when a row's
-// max grows by more than 2^8), and caught up to the exact phase-1 max before
-// phase 2, so phase 2 sees the same running max sequence as the reference.
-// The K/V tiles of block i+1 are fetched into registers while block i computes.
 // Workgroups are mapped XCD-aware: each XCD walks a contiguous run of query
 // blocks of the same head.
 //
+// Two kernels.  k4_sparse_attn_dma (D = 128) loads K/V tiles straight into LDS
+// (buffer_load ... lds, XOR-swizzled rows), double-buffered between the K and V
+// tiles, with an exact online softmax.  At BT = 64 it runs two query blocks per
+// four-wave workgroup (PAIR), each wave pair on its own selected tiles in lock
+// step: co-resident workgroups on a CU drift into start-time cohorts, each sweeping
+// a different region of key space, and pairing halves the number of cohorts (and so
+// the L2 working set), while each group's phase-2 operands are loaded once for both
+// blocks.  k4_sparse_attn (D = 64) stages tiles through registers and updates the
+// exponentiation max lazily (when a row's max grows by more than 2^8), caught up to
+// the exact phase-1 max before phase 2.
+//
 // Phase-2 operands (kbar, V^ transposed, Hbar transposed; bf16) are packed per
-// (slice, group) by k4_pack into the exact LDS image K4 copies in.
+// (slice, group) by k4_pack / k4_pack_xor into the exact LDS image K4 copies in.
 #include "common.h"
 #include "kernels.h"
 
@@ -108,16 +115,17 @@ __global__ __launch_bounds__(256) void k4_pack(const float* __restrict__ kc,
 // Phase-2 pack image for the D = 128 direct-load kernel, split between its two
 // LDS tile buffers: [Hbar^T: 128 rows x 256 B, XOR layout of a K tile] -> K buffer;
 // [kbar: 32 rows x 256 B, XOR layout][V^ transposed: PadTile<32>] -> V buffer.
+// Both parts are whole multiples of 4 KB, so the waves of a two- or four-wave
+// workgroup split their 1 KB direct loads evenly.
 template <int BT>
 struct K4DPack {
-  static constexpr int WAVES = BT / 32;
   static constexpr int HT_BYTES = 128 * 256;
   static constexpr int KB_OFF = 0;                       // within the V-buffer part
   static constexpr int VT_OFF = 32 * 256;
   static constexpr int RAW2 = VT_OFF + PadTile<kGroup>::bytes(128);
-  static constexpr int PART2 = (RAW2 + 1024 * WAVES - 1) / (1024 * WAVES) * (1024 * WAVES);
+  static constexpr int PART2 = (RAW2 + 4095) / 4096 * 4096;
   static constexpr int BYTES = HT_BYTES + PART2;
-  static_assert(HT_BYTES % (1024 * WAVES) == 0, "pack split");
+  static_assert(HT_BYTES % 4096 == 0, "pack split");
 };
 
 // Byte offset of element (row, col) in a 256-byte-row tile whose 16-byte chunk c
@@ -535,22 +543,27 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
 // c at c ^ 4*(r & 3) (conflict-free transposing reads).  The phase-2 pack image
 // is loaded the same way.
 
-template <int BT>
+// PAIR: two query blocks per workgroup, one wave group (QWAVES waves) each, with
+// their K/V tiles side by side in the K and V buffers.
+template <int BT, bool PAIR = false>
 struct K4D {
   static constexpr int D = 128;
-  static constexpr int WAVES = BT / 32;
+  static constexpr int QWAVES = BT / 32;                   // waves of one query block
+  static constexpr int QBLOCKS = PAIR ? 2 : 1;             // query blocks per workgroup
+  static constexpr int WAVES = QWAVES * QBLOCKS;
   static constexpr int THREADS = WAVES * 64;
-  static constexpr int TILE = BT * 256;                   // bytes of one K or V tile
-  static constexpr int VW = 4 / WAVES;                    // 4-row load slots per wave per 16 rows
-  static constexpr int TILE_LOADS = TILE / 1024 / WAVES;  // 1 KB direct loads per wave per tile
+  static constexpr int TILE = BT * 256;                    // bytes of one K or V tile
+  static constexpr int VW = 4 / QWAVES;                    // 4-row load slots per wave per 16 rows
+  static constexpr int TILE_LOADS = TILE / 1024 / QWAVES;  // 1 KB direct loads per wave per tile
   using PK = K4DPack<BT>;
-  // BT = 64: Hbar^T goes through the K buffer in two 16 KB halves, so that the
-  // workgroup's LDS fits four two-wave workgroups on a CU.
-  static constexpr int HT_PARTS = BT == 64 ? 2 : 1;
+  // Two-wave workgroups: Hbar^T goes through the K buffer in two 16 KB halves, so
+  // that the workgroup's LDS fits four of them on a CU.
+  static constexpr int HT_PARTS = WAVES == 2 ? 2 : 1;
   static constexpr int HT_PART = PK::HT_BYTES / HT_PARTS;
-  static constexpr int KBUF = TILE > HT_PART ? TILE : HT_PART;
-  static constexpr int VBUF = TILE > PK::PART2 ? TILE : PK::PART2;
+  static constexpr int KBUF = QBLOCKS * TILE > HT_PART ? QBLOCKS * TILE : HT_PART;
+  static constexpr int VBUF = QBLOCKS * TILE > PK::PART2 ? QBLOCKS * TILE : PK::PART2;
   static_assert(TILE_LOADS == 8, "load schedule");
+  static_assert(PK::PART2 % (1024 * WAVES) == 0 && HT_PART % (1024 * WAVES) == 0, "pack split");
 };
 
 
@@ -572,15 +585,22 @@ constexpr int kSchedDsRead = 0x100;
 // separate instantiation so that profiles tell the two launches apart.
 // PERM: q, k, v, o are frame-major and the attention runs on their token-major view
 // (rm); every row address goes through map_row.
-template <int BT, bool ALL, bool PERM>
+// PAIR: two consecutive query blocks per workgroup (video rows only: no text, not
+// ALL, not PERM).  Both visit NS selected tiles, so their barriers match; a pair
+// past the last block repeats it and stores nothing.  Phase 2 visits the groups
+// either block approximates; a group the other block approximates and this one
+// does not adds exact zeros here (p = 0, alpha = 1), so each block's result is the
+// one the unpaired kernel computes.
+template <int BT, bool ALL, bool PERM, bool PAIR = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
 void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                         const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
                         const uint32_t* __restrict__ selmask, uint16_t* __restrict__ o,
                         float scale, float c, int T, int NT, int NG, int NW, int xcd_chunk,
                         int gamma_literal, int text, int text_valid, int n_text_wg, int nbh, RowMap rm) {
+  static_assert(!PAIR || (!ALL && !PERM), "pairs run selected video blocks only");
   constexpr bool all_tiles = ALL;
-  using C = K4D<BT>;
+  using C = K4D<BT, PAIR>;
   using PK = typename C::PK;
   constexpr int D = 128;
   // Two distinct LDS objects, so the compiler can tell loads into one from reads of the other.
@@ -592,9 +612,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   // within themselves: [0, seg) with seg = T + text_valid, and the padding [seg, T + text).
   // The first n_text_wg workgroups (a multiple of 8) each own one tile of text query
   // rows of one segment and attend densely to that segment's keys; they are the
-  // longest-running ones, so they go first.  The rest own one query block of the video
-  // rows; wg & 7 names their XCD, and each XCD takes a contiguous run of a slice's
-  // query blocks (shared K/V tiles in its L2).
+  // longest-running ones, so they go first.  The rest own one query block (a pair of
+  // blocks with PAIR) of the video rows; wg & 7 names their XCD, and each XCD takes a
+  // contiguous run of a slice's query blocks (shared K/V tiles in its L2).
   const int wg = blockIdx.x;
   const bool dense = wg < n_text_wg;
   const int seg = T + text_valid;
@@ -620,7 +640,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     const int xcd = w & 7;
     const int slot = w >> 3;
     bh = slot / xcd_chunk;
-    qb = xcd * xcd_chunk + (slot - bh * xcd_chunk);
+    qb = (xcd * xcd_chunk + (slot - bh * xcd_chunk)) * C::QBLOCKS;
     if (qb >= NT) return;
     qrow0 = qb * BT;
     row_limit = T;
@@ -629,11 +649,15 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = PAIR ? wave / C::QWAVES : 0;  // query block of this wave within the workgroup
+  const int qw = PAIR ? wave - half * C::QWAVES : wave;  // wave within its query block
+  const bool store_rows = !PAIR || qb + half < NT;  // false for the repeat of a pair past the last block
+  const int qbw = qb + (store_rows ? half : 0);
   const int h = lane >> 5;
   const int l32 = lane & 31;
   const int Ttot = T + text;
   const int64_t slice = (int64_t)bh * Ttot * D;
-  const int qrow = qrow0 + wave * 32 + l32;
+  const int qrow = qrow0 + (qbw - qb) * BT + qw * 32 + l32;
   const bool perm = PERM && slice_permuted(rm, bh);
   const int qrow_st = perm ? map_row(qrow, rm) : qrow;  // stored row of this lane's query
 
@@ -660,26 +684,34 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   // The selection row is read-only here: constant address space -> scalar loads,
   // which wait on lgkmcnt and leave the in-flight tile loads alone.
   typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
-  const const_u32_ptr mrow = (const_u32_ptr)(selmask + ((int64_t)bh * NT + qb) * NW);
+  const const_u32_ptr mrow = (const_u32_ptr)(selmask + ((int64_t)bh * NT + qbw) * NW);
+  // PAIR: the rows of both blocks (phase 2 visits the groups either approximates).
+  const const_u32_ptr mrow0 = (const_u32_ptr)(selmask + ((int64_t)bh * NT + qb) * NW);
+  const const_u32_ptr mrow1 = (const_u32_ptr)(selmask + ((int64_t)bh * NT + min(qb + 1, NT - 1)) * NW);
 
   // Direct-load lane constants.  Load (vw, n) of this wave covers tile rows
-  // 16n + 4*(wave + WAVES*vw) + lane/16; the lane's 16 bytes land at chunk lane % 16.
+  // 16n + 4*(qw + QWAVES*vw) + lane/16 of its query block's tile; the lane's 16 bytes
+  // land at chunk lane % 16.
   const int lrow = lane >> 4;
   const int lch = lane & 15;
   uint32_t k_lane[C::VW];
 #pragma unroll
   for (int vw = 0; vw < C::VW; ++vw) {
-    const int r = 4 * (wave + C::WAVES * vw) + lrow;  // row mod 16
+    const int r = 4 * (qw + C::QWAVES * vw) + lrow;  // row mod 16
     k_lane[vw] = (uint32_t)(r * 256 + ((lch ^ r) << 4));
   }
-  const uint32_t v_lane0 = (uint32_t)((4 * wave + lrow) * 256 + ((lch ^ (4 * lrow)) << 4));
+  const uint32_t v_lane0 = (uint32_t)((4 * qw + lrow) * 256 + ((lch ^ (4 * lrow)) << 4));
 
   const u32x4_t kd = make_rsrc_words(k + slice, slice_bytes);
   const u32x4_t vd = make_rsrc_words(v + slice, slice_bytes);
   const uint32_t ks_lds = lds_addr(Ks);
   const uint32_t vs_lds = lds_addr(Vs);
+  // This query block's K and V tiles (phase 1); phase 2 uses the whole buffers.
+  const int tile_off = half * C::TILE;
+  const uint32_t kt_lds = ks_lds + tile_off;
+  const uint32_t vt_lds = vs_lds + tile_off;
   // A tile is BT key rows starting at row `row0` of the slice (rows past the slice read as zero).
-  // Permuted slices: the lane's rows row0 + 16n + 4(wave + WAVES vw) + lrow are fetched
+  // Permuted slices: the lane's rows row0 + 16n + 4(qw + QWAVES vw) + lrow are fetched
   // from their stored rows (computed for K, reused by the V load of the same tile).
   int st_row[C::VW][BT / 16];
   auto stored_rows = [&](int row0) {
@@ -687,7 +719,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
       for (int n = 0; n < BT / 16; ++n)
-        st_row[vw][n] = map_row(row0 + 16 * n + 4 * (wave + C::WAVES * vw) + lrow, rm);
+        st_row[vw][n] = map_row(row0 + 16 * n + 4 * (qw + C::QWAVES * vw) + lrow, rm);
   };
   auto load_k = [&](int row0) {
     if (perm) {
@@ -696,7 +728,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
         for (int n = 0; n < BT / 16; ++n)
-          dma_load16_lds(kd, ks_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256,
+          dma_load16_lds(kd, kt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256,
                          (uint32_t)st_row[vw][n] * 256u + (k_lane[vw] & 255u), 0u);
       return;
     }
@@ -705,7 +737,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
       for (int n = 0; n < BT / 16; ++n)
-        dma_load16_lds(kd, ks_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256, k_lane[vw] + 16 * n * 256, soff);
+        dma_load16_lds(kd, kt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256, k_lane[vw] + 16 * n * 256, soff);
   };
   auto load_v = [&](int row0) {  // permuted slices: row0 is the tile of the last load_k
     if (perm) {
@@ -713,7 +745,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
         for (int n = 0; n < BT / 16; ++n)
-          dma_load16_lds(vd, vs_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256,
+          dma_load16_lds(vd, vt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256,
                          (uint32_t)st_row[vw][n] * 256u + (v_lane0 & 255u), 0u);
       return;
     }
@@ -722,8 +754,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
       for (int n = 0; n < BT / 16; ++n)
-        dma_load16_lds(vd, vs_lds + (16 * n + 4 * (wave + C::WAVES * vw)) * 256,
-                       v_lane0 + (4 * C::WAVES * vw + 16 * n) * 256, soff);
+        dma_load16_lds(vd, vt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256,
+                       v_lane0 + (4 * C::QWAVES * vw + 16 * n) * 256, soff);
   };
 
   // MFMA operand addresses: K-layout A fragments (also used for Hbar^T and kbar)
@@ -773,6 +805,19 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   };
 
   // ---------------- Phase 1 ------------------------------------------------------
+  // PAIR: the tile count of the longer of the two selection rows.  Rows written by
+  // pasa_select all hold NS bits; a shorter row idles through its partner's extra
+  // tiles below, so that the workgroup barriers stay matched.
+  int pair_tiles = 0;
+  int tiles_done = 0;
+  if (PAIR) {
+    int n0 = 0, n1 = 0;
+    for (int w = 0; w < NW; ++w) {
+      n0 += __builtin_popcount(mrow0[w]);
+      n1 += __builtin_popcount(mrow1[w]);
+    }
+    pair_tiles = max(n0, n1);
+  }
   int nv_cur = 0;
   int blk = next_tile(nv_cur);
   if (blk >= 0) {
@@ -794,7 +839,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int ks = 0; ks < D / 16; ++ks)
 #pragma unroll
       for (int mt = 0; mt < BT / 32; ++mt) {
-        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + mt * 32 * 256));
+        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks + tile_off, kofs[ks] + mt * 32 * 256));
         sacc[mt] = mfma32(a, qf[ks], sacc[mt]);
       }
     // Keep 8 fragment reads in flight: each MFMA consumes a read issued 8 MFMAs
@@ -866,8 +911,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int s = 0; s < BT / 16; ++s)
 #pragma unroll
       for (int et = 0; et < D / 32; ++et) {
-        const uint2 lo = lds_read_tr16(Vs, vofs[et] + s * 16 * 256);
-        const uint2 hi = lds_read_tr16(Vs, vofs[et] + s * 16 * 256 + 8 * 256);
+        const uint2 lo = lds_read_tr16(Vs + tile_off, vofs[et] + s * 16 * 256);
+        const uint2 hi = lds_read_tr16(Vs + tile_off, vofs[et] + s * 16 * 256 + 8 * 256);
         const bf16x8_t a = __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
         oacc[et] = mfma32(a, pf[s], oacc[et]);
       }
@@ -888,6 +933,12 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     if (nxt >= 0) load_v(nxt);
     blk = nxt;
     nv_cur = nv_nxt;
+    if (PAIR) ++tiles_done;
+  }
+  if (PAIR) {
+    for (; tiles_done < pair_tiles; ++tiles_done)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) barrier_lds_reads_done();  // the loop's four barriers per tile
   }
 
   // ---------------- Phase 2 ------------------------------------------------------
@@ -896,15 +947,19 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const unsigned char* Pvt = Vs + PK::VT_OFF;
   const int pv_base = PadTile<kGroup>::frag_base(l32, h);
   const int ng_run = (dense || all_tiles) ? 0 : NG;  // text rows and dense attention: no correction term
-  // Groups with at least one unselected in-range block, in ascending order.
-  auto approx_of = [&](int g) -> uint32_t {
+  // Groups with at least one unselected in-range block (of either block of a pair),
+  // in ascending order.
+  auto inrange_of = [&](int g) -> uint32_t {
     const int nin = min(kGroup, NT - g * kGroup);
-    const uint32_t inrange = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
-    return inrange & ~mrow[g];
+    return nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+  };
+  auto approx_of = [&](int g) -> uint32_t { return inrange_of(g) & ~mrow[g]; };
+  auto visit_of = [&](int g) -> uint32_t {
+    return PAIR ? inrange_of(g) & ~(mrow0[g] & mrow1[g]) : approx_of(g);
   };
   auto next_group = [&](int g) -> int {
     for (++g; g < ng_run; ++g)
-      if (approx_of(g) != 0u) return g;
+      if (visit_of(g) != 0u) return g;
     return -1;
   };
   // A group's pack is two parts: kbar + V^T (part 2, into Vs) and Hbar^T (into Ks).
@@ -1036,7 +1091,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   }
 
   const float denom = halves_sum(l_run) + halves_sum(g_run);
-  if (qrow < row_limit) {
+  if (store_rows && qrow < row_limit) {
     uint16_t* orow = o + slice + (int64_t)qrow_st * D;
 #pragma unroll
     for (int et = 0; et < D / 32; ++et)
@@ -1110,7 +1165,13 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
     hipLaunchKernelGGL((k4_sparse_attn_dma<128, false, false>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b,
                        cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
                        n_text_wg, bh, RowMap{});
-  else if (D == 128 && BT == 64)
+  else if (D == 128 && BT == 64 && text == 0) {
+    // Query blocks in pairs: each XCD takes a contiguous run of a slice's pairs.
+    const int pair_chunk = ((NT + 1) / 2 + 7) / 8;
+    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false, false, true>), dim3(8 * bh * pair_chunk),
+                       dim3(K4D<64, true>::THREADS), 0, stream, a, b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW,
+                       pair_chunk, gamma_literal, 0, 0, 0, bh, RowMap{});
+  } else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k4_sparse_attn_dma<64, false, false>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b,
                        cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
                        n_text_wg, bh, RowMap{});

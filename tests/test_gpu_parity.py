@@ -226,7 +226,9 @@ ATTN_CASES = [
     (2, (3, 10, 20), 128, 128, 0.4, "literal"),     # ragged last block
     (2, (3, 10, 20), 128, 128, 0.4, "consistent"),
     (2, (5, 13, 17), 64, 128, 0.3, "literal"),
-    (1, (9, 45, 80), 128, 64, 0.1, "literal"),      # BT 64, NT 507
+    (1, (9, 45, 80), 128, 64, 0.1, "literal"),      # BT 64, NT 507: query-block pairs, the last one a repeat
+    (2, (3, 10, 20), 128, 64, 0.4, "consistent"),   # BT 64 pairs, NT 10, ragged last block
+    (1, (1, 5, 11), 128, 64, 0.5, "literal"),       # BT 64, NT 1: one pair, its second block a repeat
     (2, (21, 30, 52), 128, 128, 0.15, "literal"),   # c1 shape, 2 heads
 ]
 
@@ -245,6 +247,37 @@ def test_sparse_attn_shared_selection(device, heads, grid, D, BT, density, gamma
     rp = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, gamma=gamma, indices=idx, ref_precision=True)
     floor = O.parity_metrics(rp, ref)
     check_parity(o.cpu(), ref, f"K4 {wl.seq_len}x{D} BT{BT} {gamma}", floor)
+
+
+def test_pair_rows_with_unequal_tile_counts(device):
+    """BT 64 runs two query blocks per workgroup in lock step.  Rows of a pair with
+    different numbers of selected blocks (never written by pasa_select, whose rows all
+    hold NS bits) still give each block its own result: odd blocks here drop their
+    lowest-scoring selection."""
+    heads, grid, D, BT, density = 2, (3, 10, 20), 128, 64, 0.4
+    wl, (q, k, v) = bf16_inputs(heads, grid, D, BT, seed=3)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    scale = D ** -0.5
+    st = ops.block_stats(qd, kd, vd, BT, 32)
+    sel = ops.select_blocks(st, density, scale)
+    NT, NS = st.qc.shape[2], sel.ns
+    assert NS >= 2
+    idx = sel.idx.cpu()
+    short = idx[..., :NS - 1].contiguous()
+    m_full = O.selection_mask(idx, NT)
+    m_short = O.selection_mask(short, NT)
+    mask = m_full.copy()
+    mask[..., 1::2, :] = m_short[..., 1::2, :]
+    say(f"[K4] unequal pair rows: heads={heads} NT={NT} NS={NS} (odd blocks NS-1)")
+    sel2 = ops.Selection(idx=sel.idx, selmask=torch.from_numpy(mask.view(np.int32)).to(device), scores=None,
+                         ns=NS)
+    o = ops.sparse_attn(qd, kd, vd, st, sel2, scale, BT, "literal").cpu()
+    ref_full = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, indices=idx)
+    ref_short = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, indices=short)
+    T = wl.seq_len
+    odd_rows = ((torch.arange(T) // BT) % 2 == 1)[None, None, :, None]
+    ref = torch.where(odd_rows, ref_short, ref_full)
+    check_parity(o, ref, "K4 BT64 pairs with unequal rows")
 
 
 def test_full_density_equals_dense_attention(device):
