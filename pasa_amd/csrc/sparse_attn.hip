@@ -556,14 +556,11 @@ struct K4D {
   static constexpr int VW = 4 / QWAVES;                    // 4-row load slots per wave per 16 rows
   static constexpr int TILE_LOADS = TILE / 1024 / QWAVES;  // 1 KB direct loads per wave per tile
   using PK = K4DPack<BT>;
-  // Two-wave workgroups: Hbar^T goes through the K buffer in two 16 KB halves, so
-  // that the workgroup's LDS fits four of them on a CU.
-  static constexpr int HT_PARTS = WAVES == 2 ? 2 : 1;
-  static constexpr int HT_PART = PK::HT_BYTES / HT_PARTS;
-  static constexpr int KBUF = QBLOCKS * TILE > HT_PART ? QBLOCKS * TILE : HT_PART;
+  static constexpr int KBUF = QBLOCKS * TILE > PK::HT_BYTES ? QBLOCKS * TILE : PK::HT_BYTES;
   static constexpr int VBUF = QBLOCKS * TILE > PK::PART2 ? QBLOCKS * TILE : PK::PART2;
   static_assert(TILE_LOADS == 8, "load schedule");
-  static_assert(PK::PART2 % (1024 * WAVES) == 0 && HT_PART % (1024 * WAVES) == 0, "pack split");
+  static_assert(WAVES == 4, "four-wave workgroups (BT = 128, or BT = 64 in pairs)");
+  static_assert(PK::PART2 % (1024 * WAVES) == 0 && PK::HT_BYTES % (1024 * WAVES) == 0, "pack split");
 };
 
 
@@ -585,9 +582,11 @@ constexpr int kSchedDsRead = 0x100;
 // separate instantiation so that profiles tell the two launches apart.
 // PERM: q, k, v, o are frame-major and the attention runs on their token-major view
 // (rm); every row address goes through map_row.
-// PAIR: two consecutive query blocks per workgroup (video rows only: no text, not
-// ALL, not PERM).  Both visit NS selected tiles, so their barriers match; a pair
-// past the last block repeats it and stores nothing.  Phase 2 visits the groups
+// PAIR: two consecutive query blocks (or text query tiles) per workgroup (not ALL,
+// not PERM).  Video blocks visit NS selected tiles each, so their barriers match
+// (a shorter selection row, or a text pair spanning the prompt and the padding
+// segment, idles through its partner's extra tiles); a pair past the last block
+// repeats it and stores nothing.  Phase 2 visits the groups
 // either block approximates; a group the other block approximates and this one
 // does not adds exact zeros here (p = 0, alpha = 1), so each block's result is the
 // one the unpaired kernel computes.
@@ -618,14 +617,27 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const int wg = blockIdx.x;
   const bool dense = wg < n_text_wg;
   const int seg = T + text_valid;
-  int bh, qb, qrow0, row_limit, kbeg = 0, kend = seg;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = PAIR ? wave / C::QWAVES : 0;  // query block (tile) of this wave within the workgroup
+  const int qw = PAIR ? wave - half * C::QWAVES : wave;  // wave within its query block
+  // A pair's second block (tile) past the last one repeats it and stores nothing.
+  bool store_rows = true;
+  int bh, qb, qbw = 0, qrow0, row_limit, kbeg = 0, kend = seg;
+  int pair_tiles = 0;  // PAIR: tiles of the longer half (the shorter one idles through the rest)
   if (dense) {
     const int vtiles = (text_valid + BT - 1) / BT;
     const int qtiles = vtiles + (text - text_valid + BT - 1) / BT;
-    bh = wg / qtiles;
+    const int units = (qtiles + C::QBLOCKS - 1) / C::QBLOCKS;
+    bh = wg / units;
     if (bh >= nbh) return;  // padding of the text range to a multiple of 8
     qb = 0;
-    const int qt = wg - bh * qtiles;
+    const int t0 = (wg - bh * units) * C::QBLOCKS;
+    store_rows = t0 + half < qtiles;
+    const int qt = store_rows ? t0 + half : t0;
+    auto seg_tiles = [&](int t) { return t < vtiles ? (seg + BT - 1) / BT : (T + text - seg + BT - 1) / BT; };
+    if (PAIR) pair_tiles = max(seg_tiles(t0), seg_tiles(min(t0 + 1, qtiles - 1)));
     if (qt < vtiles) {
       qrow0 = T + qt * BT;
       row_limit = seg;
@@ -642,22 +654,17 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     bh = slot / xcd_chunk;
     qb = (xcd * xcd_chunk + (slot - bh * xcd_chunk)) * C::QBLOCKS;
     if (qb >= NT) return;
-    qrow0 = qb * BT;
+    store_rows = qb + half < NT;
+    qbw = qb + (store_rows ? half : 0);
+    qrow0 = qbw * BT;
     row_limit = T;
   }
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = PAIR ? wave / C::QWAVES : 0;  // query block of this wave within the workgroup
-  const int qw = PAIR ? wave - half * C::QWAVES : wave;  // wave within its query block
-  const bool store_rows = !PAIR || qb + half < NT;  // false for the repeat of a pair past the last block
-  const int qbw = qb + (store_rows ? half : 0);
   const int h = lane >> 5;
   const int l32 = lane & 31;
   const int Ttot = T + text;
   const int64_t slice = (int64_t)bh * Ttot * D;
-  const int qrow = qrow0 + (qbw - qb) * BT + qw * 32 + l32;
+  const int qrow = qrow0 + qw * 32 + l32;
   const bool perm = PERM && slice_permuted(rm, bh);
   const int qrow_st = perm ? map_row(qrow, rm) : qrow;  // stored row of this lane's query
 
@@ -805,18 +812,18 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   };
 
   // ---------------- Phase 1 ------------------------------------------------------
-  // PAIR: the tile count of the longer of the two selection rows.  Rows written by
-  // pasa_select all hold NS bits; a shorter row idles through its partner's extra
-  // tiles below, so that the workgroup barriers stay matched.
-  int pair_tiles = 0;
+  // PAIR: the tile count of the longer half: for video blocks the longer of the two
+  // selection rows (rows written by pasa_select all hold NS bits) plus the prompt
+  // tiles; for text tiles, set above from the two segments.  The shorter half idles
+  // through its partner's extra tiles below, so that the workgroup barriers match.
   int tiles_done = 0;
-  if (PAIR) {
+  if (PAIR && !dense) {
     int n0 = 0, n1 = 0;
     for (int w = 0; w < NW; ++w) {
       n0 += __builtin_popcount(mrow0[w]);
       n1 += __builtin_popcount(mrow1[w]);
     }
-    pair_tiles = max(n0, n1);
+    pair_tiles = max(n0, n1) + (text_valid + BT - 1) / BT;
   }
   int nv_cur = 0;
   int blk = next_tile(nv_cur);
@@ -964,11 +971,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   };
   // A group's pack is two parts: kbar + V^T (part 2, into Vs) and Hbar^T (into Ks).
   // Part 2 of the next group loads while this group's Hbar^T product runs, and the
-  // next Hbar^T loads while the next group's scores and P.V^ run.  With HT_PARTS = 2
-  // the second half of Hbar^T (feature rows 64-127) follows the first through Ks.
-  constexpr int HT_PARTS = C::HT_PARTS;
-  constexpr int ETP = (D / 32) / HT_PARTS;  // 32-row output tiles per part
-  constexpr int HT_LOADS = C::HT_PART / 1024 / C::WAVES;
+  // next Hbar^T loads while the next group's scores and P.V^ run.
+  constexpr int HT_LOADS = PK::HT_BYTES / 1024 / C::WAVES;
   constexpr int P2_LOADS = PK::PART2 / 1024 / C::WAVES;
   auto load_part2 = [&](int g) {
     const uint32_t gsoff = (uint32_t)(g * PK::BYTES);
@@ -978,8 +982,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       dma_load16_lds(pd, vs_lds + kb * 1024, (uint32_t)(PK::HT_BYTES + kb * 1024 + lane * 16), gsoff);
     }
   };
-  auto load_ht = [&](int g, int part) {
-    const uint32_t gsoff = (uint32_t)(g * PK::BYTES + part * C::HT_PART);
+  auto load_ht = [&](int g) {
+    const uint32_t gsoff = (uint32_t)(g * PK::BYTES);
 #pragma unroll
     for (int n = 0; n < HT_LOADS; ++n) {
       const int kb = n * C::WAVES + wave;  // 1 KB piece of Hbar^T
@@ -989,7 +993,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   int g = next_group(-1);
   if (g >= 0) {  // phase 1 ended with a barrier after the last reads of Ks and Vs
     load_part2(g);
-    load_ht(g, 0);
+    load_ht(g);
   }
   while (g >= 0) {
     const int gn = next_group(g);
@@ -1061,32 +1065,24 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     barrier_lds_reads_done();
 
     const float f = psum * scale;
+    f32x16_t racc[D / 32];
 #pragma unroll
-    for (int part = 0; part < HT_PARTS; ++part) {
-      if (part > 0) {  // the next half of this group's Hbar^T (part 2 of gn, issued earlier, lands first)
-        load_ht(g, part);
-        wait_vmcnt<0>();
-        barrier_lds_reads_done();
+    for (int et = 0; et < D / 32; ++et)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) racc[et][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int et = 0; et < D / 32; ++et) {
+        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
+        racc[et] = mfma32(a, qf[ks], racc[et]);
       }
-      f32x16_t racc[ETP];
 #pragma unroll
-      for (int et = 0; et < ETP; ++et)
+    for (int et = 0; et < D / 32; ++et)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) racc[et][r] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-        for (int et = 0; et < ETP; ++et) {
-          const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
-          racc[et] = mfma32(a, qf[ks], racc[et]);
-        }
-#pragma unroll
-      for (int et = 0; et < ETP; ++et)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[part * ETP + et][r] = fmaf(racc[et][r], f, oacc[part * ETP + et][r]);
-      barrier_lds_reads_done();  // every wave is done reading this part of Hbar^T
-    }
-    if (gn >= 0) load_ht(gn, 0);
+      for (int r = 0; r < 16; ++r) oacc[et][r] = fmaf(racc[et][r], f, oacc[et][r]);
+    barrier_lds_reads_done();  // every wave is done reading Hbar^T
+    if (gn >= 0) load_ht(gn);
     g = gn;
   }
 
@@ -1165,16 +1161,15 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
     hipLaunchKernelGGL((k4_sparse_attn_dma<128, false, false>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b,
                        cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
                        n_text_wg, bh, RowMap{});
-  else if (D == 128 && BT == 64 && text == 0) {
-    // Query blocks in pairs: each XCD takes a contiguous run of a slice's pairs.
+  else if (D == 128 && BT == 64) {
+    // Query blocks (and text tiles) in pairs: each XCD takes a contiguous run of a
+    // slice's pairs.
     const int pair_chunk = ((NT + 1) / 2 + 7) / 8;
-    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false, false, true>), dim3(8 * bh * pair_chunk),
+    const int n_text_pairs = (bh * ((text_qtiles + 1) / 2) + 7) / 8 * 8;
+    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false, false, true>), dim3(n_text_pairs + 8 * bh * pair_chunk),
                        dim3(K4D<64, true>::THREADS), 0, stream, a, b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW,
-                       pair_chunk, gamma_literal, 0, 0, 0, bh, RowMap{});
-  } else if (D == 128 && BT == 64)
-    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false, false>), grid, dim3(K4D<64>::THREADS), 0, stream, a, b,
-                       cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
-                       n_text_wg, bh, RowMap{});
+                       pair_chunk, gamma_literal, text, text_valid, n_text_pairs, bh, RowMap{});
+  }
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
   else if (D == 64 && BT == 64)
