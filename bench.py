@@ -235,7 +235,8 @@ def main() -> int:
         import dataclasses
         others = {}
         for name, w in (("c1", WORKLOADS["c1"]), ("c3", WORKLOADS["c3"]),
-                        ("c2_block64", dataclasses.replace(wl, block_size=64))):
+                        ("c2_block64", dataclasses.replace(wl, block_size=64)),
+                        ("c3_block64", dataclasses.replace(WORKLOADS["c3"], block_size=64))):
             others[name] = config_step(torch, ops, make_inputs, w, dev, args.seed)
             log(f"{name}: {others[name]['ms_per_step']:.3f} ms/step, {others[name]['TFLOPs_effective']:.1f} "
                 f"TFLOP/s effective, K4 {others[name]['k4_ms']:.3f} ms")
