@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void k4_pack(const float* __restrict__ kc,
 // Phase-2 pack image for the D = 128 direct-load kernel, split between its two
 // LDS tile buffers: [Hbar^T: 128 rows x 256 B, XOR layout of a K tile] -> K buffer;
 // [kbar: 32 rows x 256 B, XOR layout][V^ transposed: PadTile<32>] -> V buffer.
-// Both parts are whole multiples of 4 KB, so the waves of a two- or four-wave
+// Both parts are whole multiples of 4 KB, so the four waves of a
 // workgroup split their 1 KB direct loads evenly.
 template <int BT>
 struct K4DPack {
