@@ -124,7 +124,7 @@ template <int KPL>
 __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, int NT, int NS, int NSP,
                                               int NW, int32_t* __restrict__ idx,
                                               uint32_t* __restrict__ selmask) {
-  constexpr int kCopies = 8;
+  constexpr int kCopies = 2;
   extern __shared__ uint64_t sel[];
   __shared__ uint32_t hist[kCopies][256];
   __shared__ uint32_t words[kMaxSelectBlocks / 32];
