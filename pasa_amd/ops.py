@@ -191,6 +191,33 @@ def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_t
     return pack
 
 
+def _check_out(v: torch.Tensor, out: Optional[torch.Tensor]) -> torch.Tensor:
+    """The output buffer: a new tensor like ``v``, or ``out`` if it matches ``v`` exactly
+    (the kernels store every row of it without bounds checks)."""
+    if out is None:
+        return torch.empty_like(v)
+    _check_device(out)
+    if out.shape != v.shape or out.dtype != v.dtype or out.device != v.device:
+        raise ValueError(f"out must be a contiguous {v.dtype} tensor of shape {tuple(v.shape)} on {v.device}, "
+                         f"got {out.dtype} {tuple(out.shape)} on {out.device}")
+    return out
+
+
+def _check_selection(sel: Selection, q: torch.Tensor, block_size: int, text_tokens: int) -> None:
+    """The selection must be the one pasa_select writes for this shape and block size:
+    K4 reads selmask rows ceil(NT/32) words apart without bounds checks."""
+    B, H, T, _ = q.shape
+    NT = math.ceil((T - int(text_tokens)) / block_size)
+    nw = (NT + 31) // 32
+    _check_device(sel.idx, sel.selmask)
+    if sel.selmask.dtype not in (torch.int32, torch.uint32) or tuple(sel.selmask.shape) != (B, H, NT, nw):
+        raise ValueError(f"selmask must be int32 [{B}, {H}, {NT}, {nw}] for block_size {block_size}, "
+                         f"got {sel.selmask.dtype} {tuple(sel.selmask.shape)}")
+    if sel.idx.dtype != torch.int32 or tuple(sel.idx.shape[:3]) != (B, H, NT) or sel.idx.dim() != 4:
+        raise ValueError(f"idx must be int32 [{B}, {H}, {NT}, ns] for block_size {block_size}, "
+                         f"got {sel.idx.dtype} {tuple(sel.idx.shape)}")
+
+
 def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: torch.Tensor,
                        sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
                        out: Optional[torch.Tensor] = None, text_tokens: int = 0,
@@ -203,8 +230,10 @@ def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: 
     if gamma not in ("literal", "consistent"):
         raise ValueError("gamma must be 'literal' or 'consistent'")
     B, H, T, D = q.shape
-    o = torch.empty_like(v) if out is None else out
-    _check_device(o)
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    _check_selection(sel, q, block_size, text_tokens)
+    o = _check_out(v, out)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(), pack.numel(), sel.idx.data_ptr(),
             sel.selmask.data_ptr(), o.data_ptr(), float(scale), B * H, T, int(text_tokens),
             int(text_tokens if text_valid is None else text_valid), D, block_size, GROUP_SIZE, sel.ns,
@@ -241,8 +270,9 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Op
     _check_device(q, k, v)
     B, H, T, D = q.shape
     scale = D ** -0.5 if scale is None else scale
-    o = torch.empty_like(v) if out is None else out
-    _check_device(o)
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    o = _check_out(v, out)
     tv = text_tokens if text_valid is None else text_valid
     _lib.call("pasa_dense_attn", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), float(scale), B * H, T,
               int(text_tokens), int(tv), D, _DTYPES.get(q.dtype, -1), _stream(q))
