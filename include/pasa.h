@@ -4,7 +4,8 @@
  * Every entry point is extern "C", takes plain device pointers, sizes and a
  * hipStream_t passed as void*, and returns an int status (0 = OK, negative =
  * error, see pasa_status_t).  The library never allocates device memory: the
- * caller passes every buffer, including workspace.  All shape / dtype / size
+ * caller passes every buffer, including workspace (pasa_sparse_attn_noalloc alone
+ * uses a static device array instead, sized at load).  All shape / dtype / size
  * checks run on the host before any HIP call, so every error path is reachable
  * without a GPU.  No entry point synchronises; work is enqueued on `stream`.
  * No atomics on global memory: identical inputs give bitwise-identical outputs.
@@ -38,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 6
+#define PASA_ABI_VERSION 7
 
 typedef enum {
   PASA_OK = 0,
@@ -204,6 +205,29 @@ int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const v
                             void* o, double scale, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t text_valid, int64_t head_dim, int64_t block_size,
                             int64_t group_size, int64_t ns, int gamma_literal, int dtype, void* stream);
+
+/* pasa_sparse_attn without a workspace argument: the packed phase-2 operands live in
+ * a static device array of PASA_NOALLOC_SCRATCH_BYTES bytes that the library holds on
+ * every GPU it runs on until the process ends, so the call allocates nothing and
+ * needs no caller buffer beyond its inputs and outputs.  Its size limits the shape:
+ * bh * ceil(ceil((seq_len - text_len) / block_size) / 32) * 53,248 bytes must fit
+ * (1,260 slice-groups: the Wan2.1-14B 720p shape at block size 128, 760; HunyuanVideo
+ * 720p at block size 128, 720; Wan2.1-1.3B at block size 64, 192); a larger shape
+ * returns PASA_ERR_WORKSPACE before any launch.  Calls on one GPU share its array,
+ * so calls that overlap on one GPU race; calls in stream order do not.  The first
+ * call on a device looks the array's address up (hipGetSymbolAddress) and caches it.
+ * Arguments and results otherwise as pasa_sparse_attn (same kernels, bitwise-equal
+ * output).
+ * No counterpart in the reference: this entry is for callers that cannot allocate
+ * device memory, such as code under HIP graph capture and tight serving loops. */
+#define PASA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int pasa_sparse_attn_noalloc(const void* q, const void* k, const void* v,
+                             const float* kc, const float* vc, const float* hgroup,
+                             const int32_t* idx, const uint32_t* selmask, void* o,
+                             double scale, int64_t bh, int64_t seq_len, int64_t text_len,
+                             int64_t text_valid, int64_t head_dim,
+                             int64_t block_size, int64_t group_size, int64_t ns,
+                             int gamma_literal, int dtype, void* stream);
 
 /* ---- Token-major view of frame-major tensors -------------------------------- */
 

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/pasa.h"
 #include "kernels.h"
@@ -413,6 +414,84 @@ int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* k
   return pasa_sparse_attn_packed(q, k, v, workspace, workspace_bytes, idx, selmask, o, scale, bh, seq_len,
                                  text_len, text_valid, head_dim, block_size, group_size, ns, gamma_literal,
                                  dtype, stream);
+}
+
+}  // extern "C"
+
+// ---- the allocation-free attention entry ------------------------------------
+//
+// pasa_sparse_attn_noalloc keeps its phase-2 pack in `scratch`, one static device
+// array per GPU that lives until the process ends.  In host code `scratch` names a
+// host-side stand-in, not device memory, so kernels receive the address that
+// hipGetSymbolAddress returns for the device the call runs on, looked up once per
+// device (with that device current) and cached.  Every call on one device reuses
+// that device's array: calls that overlap on one device race.  The pack kernel
+// writes every byte K4 reads, so nothing has to be cleared between calls.
+namespace {
+
+constexpr size_t kScratchBytes = PASA_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (the current device
+// for the null stream).
+int scratch_address(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PASA_ERR_LAUNCH, "pasa_sparse_attn_noalloc: device of the stream: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(PASA_ERR_BAD_ARG, "pasa_sparse_attn_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess)
+      return fail(PASA_ERR_LAUNCH, "pasa_sparse_attn_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(PASA_ERR_LAUNCH, "pasa_sparse_attn_noalloc: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess && e2 != hipSuccess) e = e2;
+    }
+    if (e != hipSuccess || p == nullptr)
+      return fail(PASA_ERR_LAUNCH, "pasa_sparse_attn_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PASA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pasa_sparse_attn_noalloc(const void* q, const void* k, const void* v, const float* kc, const float* vc,
+                             const float* hgroup, const int32_t* idx, const uint32_t* selmask, void* o,
+                             double scale, int64_t bh, int64_t seq_len, int64_t text_len, int64_t text_valid,
+                             int64_t head_dim, int64_t block_size, int64_t group_size, int64_t ns,
+                             int gamma_literal, int dtype, void* stream) {
+  if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn_noalloc: NULL pointer");
+  int rc;
+  if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, text_valid, head_dim,
+                            block_size, group_size, ns, gamma_literal, dtype)))
+    return rc;
+  const size_t need = pasa_sparse_attn_workspace_bytes(bh, seq_len, text_len, head_dim, block_size, group_size);
+  if (need > kScratchBytes)
+    return fail(PASA_ERR_WORKSPACE,
+                "pasa_sparse_attn_noalloc: the phase-2 pack needs %zu bytes, more than the %zu-byte static scratch "
+                "(call pasa_sparse_attn with a workspace instead)", need, kScratchBytes);
+  void* pack = nullptr;
+  if ((rc = scratch_address(stream, &pack))) return rc;
+  if ((rc = pasa_pack_phase2(kc, vc, hgroup, pack, kScratchBytes, bh, seq_len, text_len, head_dim, block_size,
+                             group_size, stream)))
+    return rc;
+  return pasa_sparse_attn_packed(q, k, v, pack, kScratchBytes, idx, selmask, o, scale, bh, seq_len, text_len,
+                                 text_valid, head_dim, block_size, group_size, ns, gamma_literal, dtype, stream);
 }
 
 int pasa_dense_attn(const void* q, const void* k, const void* v, void* o, double scale, int64_t bh,

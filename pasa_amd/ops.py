@@ -259,6 +259,30 @@ def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockS
                               placement)
 
 
+def sparse_attn_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockStats,
+                        sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
+                        out: Optional[torch.Tensor] = None, text_tokens: int = 0,
+                        text_valid: Optional[int] = None) -> torch.Tensor:
+    """``sparse_attn`` through ``pasa_sparse_attn_noalloc``: the phase-2 pack lives in the
+    library's static device array, so with ``out`` given the call allocates nothing
+    (for code under HIP graph capture).  Shapes whose pack exceeds
+    ``_lib.NOALLOC_SCRATCH_BYTES`` raise PasaError (PASA_ERR_WORKSPACE)."""
+    _check_device(q, k, v, stats.kc, stats.vc, stats.hgroup)
+    if gamma not in ("literal", "consistent"):
+        raise ValueError("gamma must be 'literal' or 'consistent'")
+    B, H, T, D = q.shape
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    _check_selection(sel, q, block_size, text_tokens)
+    o = _check_out(v, out)
+    _lib.call("pasa_sparse_attn_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), stats.kc.data_ptr(),
+              stats.vc.data_ptr(), stats.hgroup.data_ptr(), sel.idx.data_ptr(), sel.selmask.data_ptr(),
+              o.data_ptr(), float(scale), B * H, T, int(text_tokens),
+              int(text_tokens if text_valid is None else text_valid), D, block_size, GROUP_SIZE, sel.ns,
+              int(gamma == "literal"), _DTYPES.get(q.dtype, -1), _stream(q))
+    return o
+
+
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
                     text_tokens: int = 0, text_valid: Optional[int] = None,
                     out: Optional[torch.Tensor] = None) -> torch.Tensor:

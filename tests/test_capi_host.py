@@ -164,6 +164,44 @@ def test_sparse_attn_validation(lib, kw, code):
     assert lib.pasa_last_error()
 
 
+def attn_noalloc(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, kc=FAKE, vc=FAKE, hg=FAKE, idx=FAKE, mask=FAKE, o=FAKE, scale=0.1,
+             bh=2, T=1000, text=0, tv=None, D=128, BT=128, G=32, ns=2, lit=1, dtype=0)
+    a.update(kw)
+    tv = a["text"] if a["tv"] is None else a["tv"]
+    return lib.pasa_sparse_attn_noalloc(a["q"], a["k"], a["v"], a["kc"], a["vc"], a["hg"], a["idx"], a["mask"],
+                                        a["o"], a["scale"], a["bh"], a["T"], a["text"], tv, a["D"], a["BT"],
+                                        a["G"], a["ns"], a["lit"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(o=None), -1), (dict(kc=None), -1), (dict(dtype=2), -7), (dict(D=256), -3), (dict(BT=256), -4),
+    (dict(G=16), -12), (dict(ns=9), -5), (dict(scale=0.0), -9), (dict(lit=2), -9),
+    (dict(text=100, tv=101), -10),
+    # the pack of 1261 slice-groups (53,248 bytes each) exceeds the 64 MiB static scratch
+    (dict(bh=1261, T=4096, ns=1), -8),
+    # Wan2.1-14B 720p at block size 64: 40 slices x 37 groups
+    (dict(bh=40, T=75600, BT=64, ns=118), -8),
+])
+def test_sparse_attn_noalloc_validation(lib, kw, code):
+    assert attn_noalloc(lib, **kw) == code
+    msg = lib.pasa_last_error()
+    assert msg
+    if code == -8:
+        assert b"static scratch" in msg
+
+
+def test_noalloc_scratch_limit_matches_header(lib):
+    text = HEADER.read_text()
+    assert "#define PASA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)" in text
+    assert _lib.NOALLOC_SCRATCH_BYTES == 64 << 20
+    per_group = lib.pasa_sparse_attn_workspace_bytes(1, 4096, 0, 128, 128, 32)
+    assert per_group == 53248 and _lib.NOALLOC_SCRATCH_BYTES // per_group == 1260
+    # the shapes the header names as fitting
+    for bh, T, text, BT in [(40, 75600, 0, 128), (24, 118800 + 256, 256, 128), (12, 32760, 0, 64)]:
+        assert lib.pasa_sparse_attn_workspace_bytes(bh, T, text, 128, BT, 32) <= _lib.NOALLOC_SCRATCH_BYTES
+
+
 def test_packed_entry_validation(lib):
     pk = lib.pasa_pack_phase2
     need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 0, 128, 128, 32)
