@@ -72,18 +72,16 @@ __device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t byte_off) {
 }
 
 // Bounds-checked direct load into LDS (buffer_load_dwordx4 ... lds): lane l's
-// 16 bytes at byte_off land at lds_base + 16*l (lds_base wave-uniform); lanes
-// whose range lies outside the resource write zeros.
-__device__ __forceinline__ void buf_load16_lds(rsrc_t r, unsigned char* lds_base, uint32_t byte_off,
-                                               uint32_t soff) {
-  typedef __attribute__((address_space(3))) void* lds_ptr;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_base, 16, byte_off, soff, 0, 0);
-}
-
-// The same load issued as inline assembly, for schedules that manage vmcnt
-// themselves: the compiler then does not track these loads, so it neither
-// drains them before unrelated LDS reads nor counts them in its own waits
-// (which remain correct, as extra loads in flight only make them conservative).
+// 16 bytes at byte_off land at lds_addr + 16*l (lds_addr wave-uniform); lanes
+// whose range lies outside the resource write zeros.  Issued as inline assembly,
+// for schedules that manage vmcnt themselves: the compiler then does not track
+// these loads, so it neither drains them before unrelated LDS reads nor counts
+// them in its own waits (which remain correct, as extra loads in flight only make
+// them conservative).  m0 is a reserved register, so naming it as a clobber has
+// no effect (the compiler warns and ignores it); what keeps this safe is that no
+// kernel using this load contains a compiler-generated m0 user (its own LDS-direct
+// builtin, s_sendmsg, v_movrel ...) whose hoisted m0 value this would overwrite.
+// tests/test_m0_usage.py checks the compiled kernels for exactly that.
 // rsrc: buffer descriptor words; lds_addr: LDS byte address (wave-uniform).
 __device__ __forceinline__ void dma_load16_lds(u32x4_t rsrc, uint32_t lds_addr, uint32_t byte_off,
                                                uint32_t soff) {
