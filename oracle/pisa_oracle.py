@@ -319,7 +319,11 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
                 continue
             x = (scale * LOG2E) * torch.matmul(full[0][b, r0:r1], full[1][b, k0:k1].T)
             p = torch.exp2(x - x.amax(-1, keepdim=True))
-            o = torch.matmul(p, full[2][b, k0:k1]) / p.sum(-1, keepdim=True)
+            # ref_precision: P cast to bf16 before the P.V product, as the exact phase
+            # does (:185) and as flash attention does on the reference's dense path; the
+            # row sum stays fp32 (:184)
+            pv = _bf16(p) if ref_precision else p
+            o = torch.matmul(pv, full[2][b, k0:k1]) / p.sum(-1, keepdim=True)
             out[b, r0:r1] = _bf16(o) if ref_precision else o
     out = out.reshape(B, H, T, D)
     if return_aux:

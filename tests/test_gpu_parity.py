@@ -11,7 +11,9 @@ evaluation of the same bf16 inputs:
     printed for every case;
   * K4's error is at most 1.5x (+ one ulp) that of the oracle run at the
     reference's own precision (bf16 P, kc/vc/h_group and output), i.e. the
-    kernel adds no error beyond what the reference's design has.
+    kernel adds no error beyond what the reference's design has.  Where that
+    reference-precision error itself exceeds the 2e-2 * RMS excess bound (the
+    HunyuanVideo shape), the excess bound becomes 1.5x the floor's.
 End to end, GPU and CPU fp32 scores differ in the last ulp, so a query block may
 pick a different block at an exact or near tie; the test proves every such
 difference is a near tie and checks the other query blocks elementwise."""
@@ -39,12 +41,20 @@ def say(msg):
 
 
 def check_parity(out, ref, what, floor=None):
+    """cos >= 0.999, and the error beyond one bf16 ulp <= 2e-2 * RMS.  With ``floor``
+    (the metrics of the reference-precision oracle against the same fp32 reference):
+    max|err| <= 1.5 x the floor's + one ulp, and the excess bound is max(2e-2, 1.5 x the
+    floor's excess) * RMS -- where the reference's own bf16 roundings already exceed
+    2e-2 * RMS beyond one ulp (at the HunyuanVideo shape, near-zero outputs that come from
+    cancelling sums), the kernel is held to that floor instead."""
     m = O.parity_metrics(out, ref)
     say(f"[parity] {what}: cos={m['cos']:.7f} max_abs/rms={m['max_abs_over_rms']:.3e} "
         f"excess/rms={m['excess_over_rms']:.3e}"
-        + ("" if floor is None else f" floor max_abs/rms={floor['max_abs_over_rms']:.3e}"))
+        + ("" if floor is None else f" floor max_abs/rms={floor['max_abs_over_rms']:.3e} "
+                                    f"floor excess/rms={floor['excess_over_rms']:.3e}"))
     assert m["cos"] >= COS_MIN, (what, m)
-    assert m["excess_over_rms"] <= EXCESS_OVER_RMS, (what, m)
+    bound = EXCESS_OVER_RMS if floor is None else max(EXCESS_OVER_RMS, 1.5 * floor["excess_over_rms"])
+    assert m["excess_over_rms"] <= bound, (what, m, floor)
     if floor is not None:
         ulp = float(O.bf16_ulp(torch.tensor(ref.abs().max().item())))
         assert m["max_abs"] <= 1.5 * floor["max_abs"] + ulp, (what, m, floor)
@@ -288,35 +298,109 @@ def test_full_density_equals_dense_attention(device):
     check_parity(o.cpu(), ref, "density=1")
 
 
-def check_end_to_end(o, q, k, v, wl, gpu_idx, noise=None, what=""):
-    """Whole-op parity with the oracle's own selection; selection differences must be near ties."""
-    ref, aux = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, noise=noise,
-                                   return_aux=True, text_tokens=wl.text_tokens)
-    H, NT = q.shape[1], wl.num_blocks()
+def fp32_gamma(n):
+    """Higham's gamma_n for fp32: any order of n rounded fp32 operations (products and
+    sums) on a dot product is within gamma_n * sum|a_i b_i| of the exact value."""
+    u = 2.0 ** -24
+    return n * u / (1 - n * u)
+
+
+def score_error_bound(qc, kc, hnorm, scale, noise=None):
+    """Exact selection scores and a bound on how far any fp32 evaluation of them can be.
+
+    qc, kc: fp32 [NT, D] and hnorm fp32 [NT] as K2 wrote them (K3 reads exactly these).
+    K3 forms fl(scale * kc) first (as the reference does), then the fp32 dot product
+    with qc in some order (error <= gamma_{D+1} * sum_d |qc_d * skc_d|, products
+    included), then fl(logf(fl(h + 1e-6))) (the add's relative rounding 2^-24 moves
+    the log by at most 2^-24 after division by h + 1e-6; logf itself is within 2 ulp of
+    its result; 4 ulp are allowed), then the bias add(s) (half an ulp of |score| each).  The exact score
+    is computed in fp64 from the same fp32 inputs.  Returns (exact [NT, NT], bound
+    [NT, NT])."""
+    D = qc.shape[-1]
+    skc = (kc.float() * float(scale)).double()           # fl(scale * kc), exactly as K3 rounds it
+    q64 = qc.double()
+    dot = q64 @ skc.T
+    dot_abs = q64.abs() @ skc.abs().T
+    hp = (hnorm.float() + 1e-6).double()                  # fl(h + 1e-6)
+    lb = torch.log(hp)
+    exact = dot + lb[None, :]
+    n_adds = 1
+    if noise is not None:
+        exact = exact + noise.double()[None, :]
+        n_adds = 2
+
+    def ulp32(x):
+        return torch.exp2(torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -126))) - 23)
+
+    log_err = 2.0 ** -22 + 4 * ulp32(lb)
+    bound = fp32_gamma(D + 1) * dot_abs + log_err[None, :] + n_adds * 0.5 * ulp32(exact.abs() + dot_abs)
+    return exact, bound
+
+
+def check_selection_near_ties(st_gpu, gpu_idx, scale, ns, heads, noise=None, what=""):
+    """The GPU selection of each tested head equals the top-ns of the exact scores of
+    the GPU's own block statistics, except at near ties.  If the GPU keeps block j and
+    drops block i that the exact ranking keeps, its fp32 scores put j at or above i, so
+    exact_i - exact_j <= bound_i + bound_j must hold for every such pair."""
+    n_differ, n_rows = 0, 0
+    for i, h in enumerate(heads):
+        qc, kc, hn = (t[0, h].cpu() for t in (st_gpu.qc, st_gpu.kc, st_gpu.hnorm))
+        nz = None if noise is None else noise[0, h].cpu()
+        exact, bound = score_error_bound(qc, kc, hn, scale, nz)
+        order = torch.sort(exact, dim=-1, descending=True, stable=True)
+        gi = gpu_idx[0, i].long()
+        for I in range(exact.shape[0]):
+            mine = set(gi[I].tolist())
+            ref = set(order.indices[I, :ns].tolist())
+            n_rows += 1
+            if mine == ref:
+                continue
+            n_differ += 1
+            for j in mine - ref:
+                for r in ref - mine:
+                    gap = float(exact[I, r] - exact[I, j])
+                    lim = float(bound[I, r] + bound[I, j])
+                    assert gap <= lim, (what, h, I, j, r, gap, lim)
+    say(f"[sel] {what}: {n_differ} of {n_rows} query blocks differ from the exact-score top-{ns}, "
+        f"all within the fp32 rounding bound of a tie")
+
+
+def check_end_to_end(o, q, k, v, wl, st_gpu, gpu_idx, heads, noise=None, what="", text_valid=None,
+                     gamma="literal"):
+    """Whole-op parity on the slices ``heads`` of the GPU run (q, k, v, o and gpu_idx
+    hold those slices only; st_gpu the full GPU statistics):
+      1. the GPU selection is the exact top-k of its statistics up to rounding near ties;
+      2. with the GPU's selection, the output meets the north_star bound against the
+         fp32 oracle on every row, and stays within 1.5x (+ one ulp) of the error the
+         reference's own bf16 roundings give (the ref_precision oracle);
+      3. against the oracle's own pipeline (its statistics and selection): cosine over all
+         rows, and the excess bound on every row whose selection is the same."""
+    kw = dict(text_tokens=wl.text_tokens, text_valid=text_valid, gamma=gamma)
+    H, NT, ns = q.shape[1], wl.num_blocks(), gpu_idx.shape[-1]
+    nz = None if noise is None else noise[:, list(heads)]
+    check_selection_near_ties(st_gpu, gpu_idx, wl.op_scale, ns, heads, noise, what)
+    ref_sel = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, indices=gpu_idx, **kw)
+    rp = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, indices=gpu_idx,
+                             ref_precision=True, **kw)
+    floor = O.parity_metrics(rp, ref_sel)
+    m_sel = check_parity(o.cpu(), ref_sel, what + " (GPU selection)", floor)
+    ref, aux = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, noise=nz,
+                                   return_aux=True, **kw)
     oidx = aux["idx"].reshape(1, H, NT, -1)
-    scores = aux["scores"].reshape(1, H, NT, NT)
-    ns = oidx.shape[-1]
     differ = (torch.sort(oidx, -1).values != torch.sort(gpu_idx, -1).values).any(-1)   # [1, H, NT]
-    tol = 1e-5 * float(scores.abs().max())
-    for h, b in torch.nonzero(differ[0]).tolist():
-        row = scores[0, h, b].double()
-        thr = torch.sort(row, descending=True).values[ns - 1]
-        swapped = set(gpu_idx[0, h, b].tolist()) ^ set(oidx[0, h, b].tolist())
-        gaps = [abs(float(row[j] - thr)) for j in swapped]
-        assert max(gaps) <= tol, (what, h, b, swapped, gaps)
-    say(f"[E2E] {what}: {int(differ.sum())} of {H * NT} query blocks select differently, all at near ties")
-    m = check_parity(o.cpu(), ref, what + " (all rows)") if not differ.any() else None
-    if differ.any():
-        m = O.parity_metrics(o.cpu(), ref)
-        say(f"[E2E] {what} all rows: cos={m['cos']:.7f} max_abs/rms={m['max_abs_over_rms']:.3e}")
-        assert m["cos"] >= COS_MIN
-        keep = (~differ).repeat_interleave(wl.block_size, -1)[..., : wl.video_tokens]   # [1, H, Tv]
-        keep = torch.cat([keep, keep.new_ones(*keep.shape[:-1], wl.text_tokens)], -1)  # text rows: dense
-        rms = float(ref.double().pow(2).mean().sqrt())
-        e = (o.cpu().double() - ref.double()).abs()
-        excess = float(((e - O.bf16_ulp(ref.double())).clamp_min(0)).amax(-1)[keep].max())
-        say(f"[E2E] {what} rows with identical selection: excess/rms={excess / rms:.3e}")
-        assert excess <= EXCESS_OVER_RMS * rms
+    m = O.parity_metrics(o.cpu(), ref)
+    say(f"[E2E] {what} vs the oracle's own pipeline: {int(differ.sum())} of {H * NT} query blocks select "
+        f"differently; cos={m['cos']:.7f} max_abs/rms={m['max_abs_over_rms']:.3e}")
+    assert m["cos"] >= COS_MIN
+    keep = (~differ).repeat_interleave(wl.block_size, -1)[..., : wl.video_tokens]   # [1, H, Tv]
+    keep = torch.cat([keep, keep.new_ones(*keep.shape[:-1], wl.text_tokens)], -1)  # text rows: dense
+    rms = float(ref.double().pow(2).mean().sqrt())
+    e = (o.cpu().double() - ref.double()).abs()
+    excess = float(((e - O.bf16_ulp(ref.double())).clamp_min(0)).amax(-1)[keep].max())
+    say(f"[E2E] {what} rows with identical selection: excess/rms={excess / rms:.3e}")
+    assert excess <= max(EXCESS_OVER_RMS, 1.5 * floor["excess_over_rms"]) * rms
+    return dict(m_sel, floor_max_abs_over_rms=floor["max_abs_over_rms"],
+                kernel_over_floor=m_sel["max_abs"] / floor["max_abs"])
 
 
 def test_end_to_end_c1_two_heads_with_noise(device):
@@ -330,7 +414,7 @@ def test_end_to_end_c1_two_heads_with_noise(device):
     sel = ops.select_blocks(st, wl.density, wl.op_scale, True, noise.to(device))
     o = ops.pisa_pg_attention(qd, kd, vd, density=wl.density, block_size=wl.block_size,
                               scale=wl.op_scale, use_random=True, noise=noise.to(device))
-    check_end_to_end(o, q, k, v, wl, sel.idx.cpu(), noise, "c1 end-to-end")
+    check_end_to_end(o, q, k, v, wl, st, sel.idx.cpu(), (0, 1), noise, "c1 end-to-end")
 
 
 def test_end_to_end_c2_full_shape(device):
@@ -346,7 +430,46 @@ def test_end_to_end_c2_full_shape(device):
     oc = o.cpu()
     for h in (0, wl.heads - 1):
         sl = slice(h, h + 1)
-        check_end_to_end(oc[:, sl], q[:, sl], k[:, sl], v[:, sl], wl, idx[:, sl], None, f"c2 head {h}")
+        r = check_end_to_end(oc[:, sl], q[:, sl], k[:, sl], v[:, sl], wl, st, idx[:, sl], (h,), None,
+                             f"c2 head {h}")
+        say(f"[E2E] c2 head {h}: kernel/floor max-abs ratio {r['kernel_over_floor']:.3f}")
+        assert r["kernel_over_floor"] <= 1.5
+
+
+def run_heads(wl, heads, device, text_valid=None):
+    """The GPU op on the given heads of a workload (heads are independent slices, so this
+    equals running every head and keeping these), with its statistics and selection."""
+    q, k, v = make_inputs(wl, seed=0, heads=heads)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    o = ops.pisa_pg_attention(qd, kd, vd, density=wl.density, block_size=wl.block_size, scale=wl.op_scale,
+                              text_tokens=wl.text_tokens, text_valid=text_valid)
+    st = ops.block_stats(qd, kd, vd, wl.block_size, 32, text_tokens=wl.text_tokens)
+    idx = ops.select_blocks(st, wl.density, wl.op_scale).idx.cpu()
+    return q, k, v, o, st, idx
+
+
+def test_end_to_end_c3_full_shape_two_heads(device):
+    wl = WORKLOADS["c3"]
+    heads = range(0, wl.heads, wl.heads - 1)        # the first and the last head
+    say(f"[E2E] c3 full shape: heads {list(heads)} of {wl.heads}, {wl.video_tokens} video + {wl.text_tokens} text "
+        f"tokens, NT {wl.num_blocks()}")
+    q, k, v, o, st, idx = run_heads(wl, heads, device)
+    r = check_end_to_end(o, q, k, v, wl, st, idx, (0, 1), None, "c3 full shape")
+    say(f"[E2E] c3: kernel/floor max-abs ratio {r['kernel_over_floor']:.3f}")
+    assert r["kernel_over_floor"] <= 1.5
+
+
+@pytest.mark.parametrize("name,text_valid", [("c2", None), ("c3", 141)])
+def test_end_to_end_block64_one_head(device, name, text_valid):
+    """Block size 64, the processors' default: query blocks run in pairs.  At the c3 layout
+    141 of the 256 text rows are the prompt (three prompt tiles, an odd count, so one pair
+    holds the last prompt tile and the first padding tile)."""
+    wl = small_workload(WORKLOADS[name], heads=1, grid=WORKLOADS[name].grid, block_size=64)
+    say(f"[E2E] {name} shape at block 64, 1 head: {wl.video_tokens} video + {wl.text_tokens} text tokens "
+        f"(valid {text_valid}), NT {wl.num_blocks()}")
+    q, k, v, o, st, idx = run_heads(wl, range(0, 1), device, text_valid)
+    r = check_end_to_end(o, q, k, v, wl, st, idx, (0,), None, f"{name} block 64", text_valid=text_valid)
+    assert r["kernel_over_floor"] <= 1.5
 
 
 # ------------------------------------------------------------ text segment --
@@ -424,13 +547,8 @@ def test_text_padding_full_density_is_block_diagonal(device):
 def test_end_to_end_c3_one_head_text_segment(device):
     wl = small_workload(WORKLOADS["c3"], heads=1, grid=(9, 45, 80))
     say(f"[E2E] c3 layout, 1 head, {wl.video_tokens} video + {wl.text_tokens} text tokens")
-    q, k, v = make_inputs(wl, seed=0)
-    qd, kd, vd = q.to(device), k.to(device), v.to(device)
-    o = ops.pisa_pg_attention(qd, kd, vd, density=wl.density, block_size=wl.block_size, scale=wl.op_scale,
-                              text_tokens=wl.text_tokens)
-    st = ops.block_stats(qd, kd, vd, wl.block_size, 32, text_tokens=wl.text_tokens)
-    idx = ops.select_blocks(st, wl.density, wl.op_scale).idx.cpu()
-    check_end_to_end(o, q, k, v, wl, idx, None, "c3 one head")
+    q, k, v, o, st, idx = run_heads(wl, range(0, 1), device)
+    check_end_to_end(o, q, k, v, wl, st, idx, (0,), None, "c3 one head")
 
 
 # ------------------------------------------------------------ dense warm-up --

@@ -6,6 +6,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from oracle import pisa_oracle as O
+from pasa_amd import ops
 from pasa_amd import wan_dit as W
 from pasa_amd.processors import replace_wan_attention
 from pasa_amd.processors import wan as WAN
@@ -114,3 +116,69 @@ def test_dit_fused_block_ops_match_torch_block(device, restore_wan):
     c = cos(out, ref)
     print(f"[dit] fused block ops vs PyTorch block: cos={c:.7f}", flush=True)
     assert c >= 0.9999
+
+
+class LayerSpy:
+    """Records the sparse attention call of one block (a full forward makes one per block)."""
+
+    def __init__(self, fn, which):
+        self.fn, self.which, self.n, self.calls = fn, which, 0, []
+
+    def __call__(self, q, k, v, **kw):
+        o = self.fn(q, k, v, **kw)
+        if self.n == self.which:
+            self.calls.append((q.detach().clone(), k.detach().clone(), v.detach().clone(), o.detach().clone(), kw))
+        self.n += 1
+        return o
+
+
+@pytest.mark.parametrize("density", [0.05, 0.3])
+def test_dit_full_size_sparse_layer_matches_oracle(device, monkeypatch, restore_wan, density):
+    """Config c4 at its stated size: the 30-block Wan2.1-1.3B DiT at 480p / 81 frames
+    (32,760 tokens, 512 text tokens, random init), every block sparse at ``density``
+    (block 128).  Block 15's call is checked against the oracle on heads 0 and 11 with
+    the call's own selection: the north_star bound, and within 1.5x (+ one ulp) of the
+    error of the reference's own bf16 roundings.  The two densities select 12 and 76
+    key blocks per query block, so the check tells them apart (the whole-step cosine
+    against the dense model cannot: random weights make attention diffuse)."""
+    cfg = W.WanDiTConfig()
+    torch.manual_seed(0)
+    with torch.device(device):
+        model = W.WanDiT(cfg)
+    model = model.to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(0)
+    latent = W.latent_shape(81, 480, 832)
+    lat = torch.randn(1, *latent, generator=g).to(device, torch.bfloat16)
+    text = torch.randn(1, 512, cfg.text_dim, generator=g).to(device, torch.bfloat16)
+    ts = torch.tensor([952], device=device)
+    replace_wan_attention(W.WanPipelineShape(model), 480, 832, 81, first_layers_fp=0, first_times_fp=0)
+    restore_wan.block_size, restore_wan.first_times_fp = 128, 1000
+    restore_wan.rescaled_density = {952: density}
+    spy = LayerSpy(WAN.pisa_pg_attention, which=15)
+    monkeypatch.setattr(WAN, "pisa_pg_attention", spy)
+    print(f"[dit] c4 full size, density {density}: {cfg.num_layers} blocks, forward", flush=True)
+    with torch.no_grad():
+        out = model(lat, ts, text)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert spy.n == cfg.num_layers and len(spy.calls) == 1
+    q, k, v, o, kw = spy.calls[0]
+    assert q.shape == (1, 12, 32760, 128)
+    assert kw == dict(density=density, block_size=128, use_random=False)
+    scale = 128 ** -0.5
+    st = ops.block_stats(q, k, v, 128, 32)
+    sel = ops.select_blocks(st, density, scale)            # deterministic: the call's own selection
+    assert sel.ns == O.num_selected(density, 256)
+    for h in (0, 11):
+        qh, kh, vh = (t[:, h:h + 1].cpu().float() for t in (q, k, v))
+        idx = sel.idx[:, h:h + 1].cpu()
+        ref = O.pisa_pg_attention(qh, kh, vh, density, 128, 32, scale, indices=idx)
+        rp = O.pisa_pg_attention(qh, kh, vh, density, 128, 32, scale, indices=idx, ref_precision=True)
+        m = O.parity_metrics(o[:, h:h + 1].cpu().float(), ref)
+        fl = O.parity_metrics(rp, ref)
+        ulp = float(O.bf16_ulp(torch.tensor(ref.abs().max().item())))
+        print(f"[dit] block 15 head {h} density {density} (NS {sel.ns}): cos={m['cos']:.7f} "
+              f"excess/rms={m['excess_over_rms']:.3e} max_abs/rms={m['max_abs_over_rms']:.3e} "
+              f"floor max_abs/rms={fl['max_abs_over_rms']:.3e}", flush=True)
+        assert m["bound_ok"], m
+        assert m["max_abs"] <= 1.5 * fl["max_abs"] + ulp, (m, fl)

@@ -252,3 +252,61 @@ def test_text_padding_is_block_diagonal_for_text_rows():
     torch.testing.assert_close(out2[..., :seg, :], out[..., :seg, :], rtol=0, atol=0)
     full = O.pisa_pg_attention(q, k, v, 0.25, 16, 2, s, dtype=f64, text_tokens=30)
     assert not torch.allclose(full[..., :Tv, :], out[..., :Tv, :])   # padding keys matter when unmasked
+
+
+def test_literal_gamma_known_answer():
+    """A hand-worked case of the literal (never rescaled) Gamma, group_pisa_attention.py
+    :201 (g_l starts at 0), :231-235 (the running max rescales acc and l_i only),
+    :242-243 (g_l += sum p-bar * n), :258-259 (o = acc / (l_i + g_l)).
+
+    One channel, blocks of one token, groups of one block; scale = 1 / LOG2E so that the
+    base-2 score is c * q * k = q * k.  q = 1 everywhere, keys 0, 1, 2 with values 1, 2, 4,
+    and every query block selects block 0.  Then for every row:
+      phase 1: m = 0, l = 1, acc = 1;
+      group 1 (mean score 1 > m): acc, l *= 2^-1 -> 0.5, 0.5; acc += 1 * 2 -> 2.5; g_l = 1 * 1 = 1;
+      group 2 (mean score 2 > m): acc, l *= 2^-1 -> 1.25, 0.25; g_l stays 1; acc += 4 -> 5.25; g_l = 2;
+      o = 5.25 / (0.25 + 2) = 7/3.
+    With Gamma rescaled like acc and l (the 'consistent' form) g_l = 0.5 + 1 = 1.5 and
+    o = 5.25 / 1.75 = 3, which is also exact softmax attention, (1 + 2*2 + 4*4) / (1 + 2 + 4):
+    single-token blocks make the zero-order term exact and H_j = 0."""
+    q = torch.ones(1, 1, 3, 1, dtype=f64)
+    k = torch.tensor([0.0, 1.0, 2.0], dtype=f64).reshape(1, 1, 3, 1)
+    v = torch.tensor([1.0, 2.0, 4.0], dtype=f64).reshape(1, 1, 3, 1)
+    idx = torch.zeros(1, 1, 3, 1, dtype=torch.int32)
+    scale = 1.0 / O.LOG2E
+    lit = O.pisa_pg_attention(q, k, v, 1 / 3, 1, 1, scale, gamma="literal", indices=idx, dtype=f64)
+    con = O.pisa_pg_attention(q, k, v, 1 / 3, 1, 1, scale, gamma="consistent", indices=idx, dtype=f64)
+    torch.testing.assert_close(lit[0, 0, :, 0], torch.full((3,), 7 / 3, dtype=f64), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(con[0, 0, :, 0], torch.full((3,), 3.0, dtype=f64), rtol=1e-12, atol=1e-12)
+    loop = O.pisa_pg_attention_loop(q[0, 0], k[0, 0], v[0, 0], idx[0, 0], 1, 1, scale, "literal")
+    torch.testing.assert_close(loop[:, 0], torch.full((3,), 7 / 3, dtype=f64), rtol=1e-12, atol=1e-12)
+
+
+def test_reference_precision_rounds_only_where_the_reference_does():
+    """The ref_precision mode (the reference's own bf16 roundings: stored kc/vc/h_group,
+    P and P-bar before their products, the output) on the hand-worked case above:
+    every intermediate there is a power of two or a small integer, exact in bf16, so
+    only the output rounds and the result is bf16(7/3) for the literal Gamma."""
+    q = torch.ones(1, 1, 3, 1, dtype=f64)
+    k = torch.tensor([0.0, 1.0, 2.0], dtype=f64).reshape(1, 1, 3, 1)
+    v = torch.tensor([1.0, 2.0, 4.0], dtype=f64).reshape(1, 1, 3, 1)
+    idx = torch.zeros(1, 1, 3, 1, dtype=torch.int32)
+    rp = O.pisa_pg_attention(q, k, v, 1 / 3, 1, 1, 1.0 / O.LOG2E, indices=idx, dtype=f64, ref_precision=True)
+    want = torch.tensor(7 / 3, dtype=f64).to(torch.bfloat16).to(f64)
+    assert float(want) != 7 / 3
+    torch.testing.assert_close(rp[0, 0, :, 0], want.expand(3), rtol=0, atol=0)
+
+
+def test_reference_precision_text_rows_round_p():
+    """Dense text rows at the reference's precision: P is rounded to bf16 before P.V and
+    the row sum stays fp32, so the result equals that computation spelled out."""
+    g = torch.Generator().manual_seed(3)
+    T, X, D = 40, 9, 4
+    q, k, v = (torch.randn(1, 1, T, D, generator=g, dtype=f64) for _ in range(3))
+    out = O.pisa_pg_attention(q, k, v, 0.5, 8, 2, 0.5, dtype=f64, text_tokens=X, ref_precision=True)
+    x = (0.5 * O.LOG2E) * (q[0, 0, T - X:] @ k[0, 0].T)
+    p = torch.exp2(x - x.amax(-1, keepdim=True))
+    pb = p.to(torch.bfloat16).to(f64)
+    want = ((pb @ v[0, 0]) / p.sum(-1, keepdim=True)).to(torch.bfloat16).to(f64)
+    torch.testing.assert_close(out[0, 0, T - X:], want, rtol=0, atol=0)
+    assert not torch.equal(pb, p)
