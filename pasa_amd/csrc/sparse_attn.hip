@@ -1009,11 +1009,15 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Vs, PK::KB_OFF + kofs[ks]));
       sb = mfma32(a, qf[ks], sb);
     }
+    // Blocks of the group that are selected (or past NT) drop out: element r of a lane
+    // in half h holds block mfma32_row(r, h) = 8(r >> 2) + 4h + (r & 3), so its keep
+    // mask is one sign-extended bit of approx >> 4h.
+    const uint32_t ah = approx >> (4 * h);
     float gmx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int mm = mfma32_row(r, h);
-      if (!((approx >> mm) & 1u)) sb[r] = -INFINITY;
+      const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe((int)ah, 8 * (r >> 2) + (r & 3), 1);
+      sb[r] = __uint_as_float((__float_as_uint(sb[r]) & keep) | (~keep & 0xff800000u));  // -inf if dropped
       gmx = fmaxf(gmx, sb[r]);
     }
     const float m_new = fmaxf(m_run, halves_max(gmx) * c);
@@ -1028,7 +1032,6 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
     }
     float psum = 0.f;
-    float gsum = 0.f;
     bf16x8_t pbf[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -1038,13 +1041,23 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         const int r0 = 8 * s + 2 * i;
         const float p0 = fast_exp2(fmaf(sb[r0], c, -m_new));
         const float p1 = fast_exp2(fmaf(sb[r0 + 1], c, -m_new));
-        const int j0 = g * kGroup + mfma32_row(r0, h);
-        const int j1 = g * kGroup + mfma32_row(r0 + 1, h);
         psum += p0 + p1;
-        gsum += p0 * (float)(j0 == NT - 1 ? last_len : BT) + p1 * (float)(j1 == NT - 1 ? last_len : BT);
         w[i] = pack_bf16x2(p0, p1);
       }
       pbf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+    }
+    // Gamma += sum_j p_j * n_j.  Every block holds BT rows except the last one, NT - 1,
+    // which holds last_len: BT * sum(p) (exact, BT being a power of two), corrected for
+    // that block in the one group holding it.
+    float gsum = psum * (float)BT;
+    if (g == NG - 1 && last_len != BT) {
+      const int mm_last = (NT - 1) - g * kGroup;
+      const int r_last = ((mm_last >> 3) << 2) | (mm_last & 3);
+      float sl = sb[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r)
+        if (r == r_last) sl = sb[r];
+      if (h == ((mm_last >> 2) & 1)) gsum += fast_exp2(fmaf(sl, c, -m_new)) * (float)(last_len - BT);
     }
     g_run += gsum;
     psum = halves_sum(psum);
@@ -1086,7 +1099,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     g = gn;
   }
 
-  const float denom = halves_sum(l_run) + halves_sum(g_run);
+  // O = A / (L + Gamma): one correctly rounded reciprocal per row, then products.
+  const float inv = 1.f / (halves_sum(l_run) + halves_sum(g_run));
   if (store_rows && qrow < row_limit) {
     uint16_t* orow = o + slice + (int64_t)qrow_st * D;
 #pragma unroll
@@ -1095,8 +1109,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int rq = 0; rq < 4; ++rq) {
         const int e0 = et * 32 + 8 * rq + 4 * h;
         uint2 w;
-        w.x = pack_bf16x2(oacc[et][4 * rq + 0] / denom, oacc[et][4 * rq + 1] / denom);
-        w.y = pack_bf16x2(oacc[et][4 * rq + 2] / denom, oacc[et][4 * rq + 3] / denom);
+        w.x = pack_bf16x2(oacc[et][4 * rq + 0] * inv, oacc[et][4 * rq + 1] * inv);
+        w.y = pack_bf16x2(oacc[et][4 * rq + 2] * inv, oacc[et][4 * rq + 3] * inv);
         *(uint2*)(orow + e0) = w;
       }
   }
