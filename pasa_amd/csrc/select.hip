@@ -9,11 +9,14 @@
 //
 // Stage 1 (k3_scores): a 64x64-tile fp32 GEMM per (slice, tile) on the fp32 MFMA,
 //   with a fixed d-order, plus the per-key-block log bias.
-// Stage 2 (k3_topk): one wavefront per row finds the NS-th largest score with a
-//   4-pass radix select over the orderable 32-bit score, takes the ties at it by
-//   lowest index, sorts the NS selected 64-bit keys (orderable(score) << 32 | ~index)
-//   with a bitonic network in LDS, and emits the indices and the selection bitmask
-//   (one bit per key block).
+// Stage 2 (k3_topk): one wavefront per row finds the NS-th largest score by a bitwise
+//   search over the orderable 32-bit score (ballot counts, narrowed to one register once
+//   the bucket holding it is small), takes the ties at it by lowest index, emits the
+//   selection bitmask (one bit per key block) from the ballots of the picks, and sorts the
+//   NS selected 64-bit keys (orderable(score) << 32 | ~index) with a bitonic network in
+//   LDS for the indices.
+#include <utility>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -94,17 +97,6 @@ __global__ __launch_bounds__(256) void k3_scores(const float* __restrict__ qc,
   }
 }
 
-// Inclusive prefix sum over the 64 lanes of a wavefront.
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t t = __shfl_up(x, d, 64);
-    if (lane >= d) x += t;
-  }
-  return x;
-}
-
 // Order-preserving map of fp32 scores to uint32 (-0.0 == +0.0).
 __device__ __forceinline__ uint32_t score_ord(float s) {
   uint32_t bits = __float_as_uint(s);
@@ -112,99 +104,106 @@ __device__ __forceinline__ uint32_t score_ord(float s) {
   return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
 }
 
-// One wavefront per row.  The row's ordered scores stay in registers (KPL per lane,
-// index j = 64 i + lane).  An MSB-first radix select over the 32-bit ordered score
-// (4 passes of 8 bits; each pass histograms the keys still matching the prefix, in
-// kCopies LDS copies picked by lane so that equal digits spread their atomics) finds
-// the NS-th largest score T and how many of the scores equal to T are taken; those
-// are the lowest indices (ties go to the lowest index).  The NS selected keys
-// (score << 32 | ~index) are compacted into LDS and sorted descending there with a
-// bitonic network.  Dynamic LDS: NSP * 8 bytes (NSP = pow2 >= NS).
-template <int KPL>
-__global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, int NT, int NS, int NSP,
-                                              int NW, int32_t* __restrict__ idx,
-                                              uint32_t* __restrict__ selmask) {
-  constexpr int kCopies = 2;
-  extern __shared__ uint64_t sel[];
-  __shared__ uint32_t hist[kCopies][256];
-  __shared__ uint32_t words[kMaxSelectBlocks / 32];
-  const int row = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int lane = threadIdx.x;
-  const float* srow = scores + ((int64_t)bh * NT + row) * NT;
+// The lanes for which c holds (as a wave-uniform mask).
+__device__ __forceinline__ uint64_t ballot(bool c) { return __builtin_amdgcn_ballot_w64(c); }
 
-  uint32_t ok[KPL];
+// op(x) over the 64 lanes: DPP exchanges within rows of 16 (lane ^ 1, lane ^ 2, then the
+// mirrors of 8 and 16 lanes), then one read per row.
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t x, Op op) {
+  x = op(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  x = op(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  x = op(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  x = op(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xf, 0xf, false));  // row_mirror
+  return op(op((uint32_t)__builtin_amdgcn_readlane((int)x, 0), (uint32_t)__builtin_amdgcn_readlane((int)x, 16)),
+            op((uint32_t)__builtin_amdgcn_readlane((int)x, 32), (uint32_t)__builtin_amdgcn_readlane((int)x, 48)));
+}
+__device__ __forceinline__ uint32_t wave_total(uint32_t x) {
+  return wave_reduce(x, [](uint32_t a, uint32_t b) { return a + b; });
+}
+
+// Number of the S register slots' values, over the whole wavefront, that are >= t.  The
+// first V slots are counted per lane in the VALU and summed across lanes once; the rest
+// by a ballot and a scalar popcount each, so that both pipes share the work.
+template <int S, int V>
+__device__ __forceinline__ uint32_t count_ge(const uint32_t (&v)[S], uint32_t t) {
+  uint32_t n = 0u;
+  if constexpr (V > 0) {
+    uint32_t c = 0u;
 #pragma unroll
-  for (int i = 0; i < KPL; ++i) {
-    const int j = i * 64 + lane;
-    ok[i] = j < NT ? score_ord(srow[j]) : 0u;
+    for (int i = 0; i < V; ++i) c += v[i] >= t ? 1u : 0u;
+    n = wave_total(c);
   }
-  for (int w = lane; w < NW; w += 64) words[w] = 0u;
+#pragma unroll
+  for (int i = V; i < S; ++i) n += (uint32_t)__popcll(ballot(v[i] >= t));
+  return n;
+}
 
-  uint32_t prefix = 0u, mask = 0u;
-  uint32_t need = (uint32_t)NS;  // rank of the threshold among the scores matching prefix
-  uint32_t* myhist = hist[lane & (kCopies - 1)];
-#pragma unroll 1
-  for (int shift = 24; shift >= 0; shift -= 8) {
+// Lanes below this one whose bit is set in m.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// x with lane L replaced by the wave-uniform v (v_writelane_b32).
+template <int L>
+__device__ __forceinline__ uint32_t write_lane(uint32_t x, uint32_t v) {
+  asm("v_writelane_b32 %0, %1, %2" : "+v"(x) : "s"(__builtin_amdgcn_readfirstlane(v)), "n"(L));
+  return x;
+}
+
+// Blocks 64 i .. 64 i + 63 are mask words 2 i (lanes 0-31 of pbs[i]) and 2 i + 1; word w
+// goes to lane w % 64 of mw[w / 64].
+template <int... I>
+__device__ __forceinline__ void set_mask_words(std::integer_sequence<int, I...>, const uint64_t* pbs,
+                                               uint32_t (&mw)[2]) {
+  ((mw[(2 * I) / 64] = write_lane<(2 * I) % 64>(mw[(2 * I) / 64], (uint32_t)pbs[I]),
+    mw[(2 * I + 1) / 64] = write_lane<(2 * I + 1) % 64>(mw[(2 * I + 1) / 64], (uint32_t)(pbs[I] >> 32))),
+   ...);
+}
+
+// The 64-bit value of lane ^ m.
+__device__ __forceinline__ uint64_t key_xor(uint64_t k, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)k, m, 64);
+  const uint32_t hi = __shfl_xor((uint32_t)(k >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic sort, descending, of the 64 R keys of a wavefront held in registers: element
+// e = R * lane + s is key[s] of that lane.  Pairs closer than R are exchanged within a
+// lane, the others across lanes (lane distance jj / R).  Keys are distinct except the
+// zero padding.
+template <int R>
+__device__ __forceinline__ void wave_sort_desc(uint64_t (&key)[R], int lane) {
+  constexpr int N = 64 * R;
 #pragma unroll
-    for (int t = 0; t < 4 * kCopies; ++t) (&hist[0][0])[t * 64 + lane] = 0u;
-    __syncthreads();
+  for (int kk = 2; kk <= N; kk <<= 1) {
 #pragma unroll
-    for (int i = 0; i < KPL; ++i)
-      if (i * 64 + lane < NT && (ok[i] & mask) == prefix) atomicAdd(&myhist[(ok[i] >> shift) & 255u], 1u);
-    __syncthreads();
-    uint32_t hb[4];
+    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+      if (jj < R) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint32_t x = 0u;
+        for (int s = 0; s < R; ++s) {
+          if (s & jj) continue;
+          const bool desc = ((R * lane + s) & kk) == 0;
+          const uint64_t a = key[s], b = key[s + jj];
+          const bool swap = desc ? (a < b) : (a > b);
+          key[s] = swap ? b : a;
+          key[s + jj] = swap ? a : b;
+        }
+      } else {
 #pragma unroll
-      for (int cp = 0; cp < kCopies; ++cp) x += hist[cp][4 * lane + t];
-      hb[t] = x;
-    }
-    const uint32_t s = hb[0] + hb[1] + hb[2] + hb[3];
-    const uint32_t incl = wave_incl_scan(s);
-    const uint32_t total = __shfl(incl, 63, 64);
-    uint32_t cum = total - incl;  // candidates in the bins of higher lanes
-    int found = -1;
-    uint32_t above = 0u;
-#pragma unroll
-    for (int t = 3; t >= 0; --t) {
-      if (found < 0 && cum < need && need <= cum + hb[t]) {
-        found = 4 * lane + t;
-        above = cum;
+        for (int s = 0; s < R; ++s) {
+          const int e = R * lane + s;
+          const uint64_t p = key_xor(key[s], jj / R);
+          const bool keep_max = ((e & jj) == 0) == ((e & kk) == 0);
+          key[s] = (keep_max == (key[s] > p)) ? key[s] : p;
+        }
       }
-      cum += hb[t];
     }
-    const uint64_t hit = __ballot(found >= 0);
-    const int src = __ffsll((long long)hit) - 1;
-    const uint32_t bin = (uint32_t)__shfl(found, src, 64);
-    need -= (uint32_t)__shfl((int)above, src, 64);
-    prefix |= bin << shift;
-    mask |= 0xffu << shift;
   }
-  // prefix = T, the NS-th largest ordered score; every score above T is selected and,
-  // of the scores equal to T, the `need` with the lowest indices.
-  uint32_t taken = 0u;  // ties at T taken so far (in index order)
-  uint32_t cnt = 0u;
-  uint64_t lt = (1ull << lane) - 1ull;
-  bool pick[KPL];
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) {
-    const bool valid = i * 64 + lane < NT;
-    const bool tie = valid && ok[i] == prefix;
-    const uint64_t tb = __ballot(tie);
-    const uint32_t rank = taken + (uint32_t)__popcll(tb & lt);
-    pick[i] = valid && (ok[i] > prefix || (tie && rank < need));
-    taken += (uint32_t)__popcll(tb);
-    cnt += pick[i] ? 1u : 0u;
-  }
-  uint32_t pos = wave_incl_scan(cnt) - cnt;
-#pragma unroll
-  for (int i = 0; i < KPL; ++i)
-    if (pick[i]) sel[pos++] = ((uint64_t)ok[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i * 64 + lane));
-  for (int i = NS + lane; i < NSP; i += 64) sel[i] = 0ull;
-  __syncthreads();
+}
 
+// Bitonic sort, descending, of sel[0, NSP) in LDS (NSP a power of two).
+__device__ __forceinline__ void lds_sort_desc(uint64_t* sel, int NSP, int lane) {
   for (int kk = 2; kk <= NSP; kk <<= 1) {
     for (int jj = kk >> 1; jj > 0; jj >>= 1) {
       for (int p = lane; p < (NSP >> 1); p += 64) {
@@ -213,24 +212,179 @@ __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, 
         const uint64_t a = sel[i];
         const uint64_t b = sel[l];
         const bool desc = (i & kk) == 0;
-        if (desc ? (a < b) : (a > b)) {
-          sel[i] = b;
-          sel[l] = a;
-        }
+        const bool swap = desc ? (a < b) : (a > b);
+        sel[i] = swap ? b : a;
+        sel[l] = swap ? a : b;
       }
       __syncthreads();
     }
   }
+}
+
+// Sorts the NS keys in sel[0, NS) (descending) and writes their indices to irow.
+template <int R>
+__device__ __forceinline__ void sort_and_store(const uint64_t* sel, int NS, int lane, int32_t* irow) {
+  uint64_t key[R];
+#pragma unroll
+  for (int s = 0; s < R; ++s) key[s] = R * lane + s < NS ? sel[R * lane + s] : 0ull;
+  wave_sort_desc<R>(key, lane);
+#pragma unroll
+  for (int s = 0; s < R; ++s)
+    if (R * lane + s < NS) irow[R * lane + s] = (int)(0xffffffffu - (uint32_t)key[s]);
+}
+
+// The picks of a row: every score above T and, when RANK, of the scores equal to T the
+// `need` with the lowest indices (without RANK every tie is taken).  The picked keys go to
+// sel in index order (a lane that does not pick writes its own slot past NSP instead, so
+// the store needs no branch); mw receives the selection mask, word w in lane w % 64 of
+// mw[w / 64].
+template <int KPL, bool RANK>
+__device__ __forceinline__ void pick_row(const uint32_t (&ok)[KPL], uint32_t T, uint32_t need, int NSP,
+                                         int lane, uint64_t* sel, uint32_t (&mw)[2]) {
+  uint32_t taken = 0u;  // ties at T taken so far (in index order)
+  uint32_t base = 0u;   // picks so far (in index order)
+  uint64_t pbs[KPL];    // ballots of the picks
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    bool pick;
+    if constexpr (RANK) {
+      const bool tie = ok[i] == T;
+      const uint64_t tb = ballot(tie);
+      pick = ok[i] > T || (tie && taken + lanes_below(tb) < need);
+      taken += (uint32_t)__popcll(tb);
+    } else {
+      pick = ok[i] >= T;  // T >= 1, so a missing key (0) is never picked
+    }
+    const uint64_t pb = ballot(pick);
+    const uint32_t pos = pick ? base + lanes_below(pb) : (uint32_t)(NSP + lane);
+    sel[pos] = ((uint64_t)ok[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i * 64 + lane));
+    base += (uint32_t)__popcll(pb);
+    pbs[i] = pb;
+  }
+  set_mask_words(std::make_integer_sequence<int, KPL>(), pbs, mw);
+}
+
+// Slots counted in the VALU per search step (the rest by ballots).
+template <int KPL>
+constexpr int kValuSlots = KPL / 3;
+
+// One wavefront per row.  The row's ordered scores stay in registers (KPL per lane,
+// index j = 64 i + lane).  The NS-th largest ordered score T is found bit by bit from
+// the top: the search keeps the bucket [prefix, prefix + 2^w) that holds T, with
+// hi = #{scores >= prefix + 2^w} and lo = #{scores >= prefix}; a step halves the
+// bucket by counting the scores >= its midpoint.  Once the bucket holds at most 64
+// scores they are compacted into one register, and the remaining bits are searched over
+// that register alone.  Every score above T is selected, and of the scores equal to T
+// the lowest indices (ties go to the lowest index).  The selection bitmask is the ballot
+// of the picks (two 32-block words per register); the NS picked keys
+// (score << 32 | ~index) are packed into LDS in index order and sorted descending in
+// registers (NS <= 256) or in LDS.  Dynamic LDS: (NSP + 64) * 8 bytes (NSP = pow2 >= NS).
+template <int KPL>
+__global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, int NT, int NS, int NSP,
+                                              int NW, int32_t* __restrict__ idx,
+                                              uint32_t* __restrict__ selmask) {
+  static_assert(KPL <= 64, "a row spans at most two 64-word mask registers");
+  extern __shared__ uint64_t sel[];
+  __shared__ uint32_t bucket[128];  // the compacted bucket, then one spill slot per lane
+  const int row = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int lane = threadIdx.x;
+  const float* srow = scores + ((int64_t)bh * NT + row) * NT;
+
+  // Missing keys (j >= NT) read as 0, below every ordered score (score_ord sets the
+  // top bit of non-negative scores and maps negative ones to ~bits, which is > 0 for
+  // every finite or infinite score; NaN scores do not occur).  The load index is
+  // clamped so that the loads need no branch.
+  uint32_t ok[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int j = i * 64 + lane;
+    const uint32_t o = score_ord(srow[min(j, NT - 1)]);
+    ok[i] = j < NT ? o : 0u;
+  }
+
+  // T = the largest t with #{j : ok_j >= t} >= NS.  Every midpoint tested is > 0, so
+  // the missing keys are never counted.  The search starts from the bits that the row's
+  // smallest and largest scores share: every score lies in that bucket.
+  uint32_t mx = 0u, mn1 = 0xffffffffu;  // max ok, min (ok - 1) (a missing key gives 2^32 - 1)
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    mx = max(mx, ok[i]);
+    mn1 = min(mn1, ok[i] - 1u);
+  }
+  mx = wave_reduce(mx, [](uint32_t a, uint32_t b) { return max(a, b); });
+  const uint32_t mn = wave_reduce(mn1, [](uint32_t a, uint32_t b) { return min(a, b); }) + 1u;
+  int w = mn == mx ? 0 : 32 - __builtin_clz(mn ^ mx);  // bits below the shared prefix
+  uint32_t prefix = w == 32 ? 0u : mn & ~((1u << w) - 1u);
+  uint32_t hi = 0u, lo = (uint32_t)NT;
+  while (w > 0 && lo - hi > 64u) {
+    --w;
+    const uint32_t mid = prefix | (1u << w);
+    const uint32_t n = count_ge<KPL, kValuSlots<KPL>>(ok, mid);
+    if (n >= (uint32_t)NS) {
+      prefix = mid;
+      lo = n;
+    } else {
+      hi = n;
+    }
+  }
+  if (w > 0) {
+    // The lo - hi <= 64 scores in [prefix, prefix + 2^w): into one register.  A score
+    // below prefix wraps to ok - prefix >= 2^32 - prefix >= 2^w (prefix + 2^w <= 2^32).
+    // Lanes whose score is outside write their own spill slot, so the store needs no
+    // branch.
+    const uint32_t span = w == 32 ? 0xffffffffu : (1u << w) - 1u;
+    uint32_t base = 0u;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const bool in = (ok[i] - prefix <= span) & (ok[i] != 0u);
+      const uint64_t m = ballot(in);
+      const uint32_t r = base + lanes_below(m);
+      bucket[in ? r : 64u + lane] = ok[i];
+      base += (uint32_t)__popcll(m);
+    }
+    __syncthreads();
+    uint32_t c[1] = {(uint32_t)lane < lo - hi ? bucket[lane] : 0u};
+    const uint32_t above = hi;  // scores above the compacted bucket
+    while (w > 0) {
+      --w;
+      const uint32_t mid = prefix | (1u << w);
+      const uint32_t n = above + count_ge<1, 0>(c, mid);
+      if (n >= (uint32_t)NS) {
+        prefix = mid;
+        lo = n;
+      } else {
+        hi = n;
+      }
+    }
+  }
+  // prefix = T; hi = #{scores > T}, lo = #{scores >= T}.  Every score above T is
+  // selected and, of the lo - hi scores equal to T, the need = NS - hi with the lowest
+  // indices (all of them when lo - hi == need, the usual case).
+  const uint32_t need = (uint32_t)NS - hi;
+  uint32_t mw[2] = {0u, 0u};
+  if (lo - hi == need)
+    pick_row<KPL, false>(ok, prefix, need, NSP, lane, sel, mw);
+  else
+    pick_row<KPL, true>(ok, prefix, need, NSP, lane, sel, mw);
+  uint32_t* mrow = selmask + ((int64_t)bh * NT + row) * NW;
+  if (lane < NW) mrow[lane] = mw[0];
+  if (64 + lane < NW) mrow[64 + lane] = mw[1];
+  __syncthreads();
 
   int32_t* irow = idx + ((int64_t)bh * NT + row) * NS;
-  for (int i = lane; i < NS; i += 64) {
-    const int j = (int)(0xffffffffu - (uint32_t)(sel[i] & 0xffffffffull));
-    irow[i] = j;
-    atomicOr(&words[j >> 5], 1u << (j & 31));
+  if (NS <= 64) {
+    sort_and_store<1>(sel, NS, lane, irow);
+  } else if (NS <= 128) {
+    sort_and_store<2>(sel, NS, lane, irow);
+  } else if (NS <= 256) {
+    sort_and_store<4>(sel, NS, lane, irow);
+  } else {
+    for (int i = NS + lane; i < NSP; i += 64) sel[i] = 0ull;
+    __syncthreads();
+    lds_sort_desc(sel, NSP, lane);
+    for (int i = lane; i < NS; i += 64) irow[i] = (int)(0xffffffffu - (uint32_t)(sel[i] & 0xffffffffull));
   }
-  __syncthreads();
-  uint32_t* mrow = selmask + ((int64_t)bh * NT + row) * NW;
-  for (int w = lane; w < NW; w += 64) mrow[w] = words[w];
 }
 
 hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,
@@ -255,21 +409,19 @@ hipError_t launch_topk(const float* scores, int bh, int NT, int NS, int32_t* idx
   if (NSP < 2) NSP = 2;
   const int NW = (NT + 31) / 32;
   dim3 grid(NT, bh);
-  const size_t lds = (size_t)NSP * sizeof(uint64_t);
+  const size_t lds = (size_t)(NSP + 64) * sizeof(uint64_t);
 #define PASA_TOPK(K) \
-  hipLaunchKernelGGL((k3_topk<K>), grid, dim3(64), lds, stream, scores, NT, NS, NSP, NW, idx, selmask)
-  if (NT <= 64 * 4)
-    PASA_TOPK(4);
-  else if (NT <= 64 * 8)
-    PASA_TOPK(8);
-  else if (NT <= 64 * 16)
-    PASA_TOPK(16);
-  else if (NT <= 64 * 32)
-    PASA_TOPK(32);
-  else if (NT <= 64 * 64)
-    PASA_TOPK(64);
-  else
-    return hipErrorInvalidValue;
+  case K:          \
+    hipLaunchKernelGGL((k3_topk<K>), grid, dim3(64), lds, stream, scores, NT, NS, NSP, NW, idx, selmask); \
+    break;
+  // Registers per lane: ceil(NT / 64) rounded up to a multiple of 4.
+  switch (4 * ((NT + 255) / 256)) {
+    PASA_TOPK(4) PASA_TOPK(8) PASA_TOPK(12) PASA_TOPK(16) PASA_TOPK(20) PASA_TOPK(24) PASA_TOPK(28)
+    PASA_TOPK(32) PASA_TOPK(36) PASA_TOPK(40) PASA_TOPK(44) PASA_TOPK(48) PASA_TOPK(52) PASA_TOPK(56)
+    PASA_TOPK(60) PASA_TOPK(64)
+    default:
+      return hipErrorInvalidValue;
+  }
 #undef PASA_TOPK
   return hipGetLastError();
 }
