@@ -188,12 +188,11 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Sum of the two bf16 halves of w, accumulated into acc (v_dot2c_f32_bf16 with ones).
-__device__ __forceinline__ float bf16x2_sum(uint32_t w, float acc) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
-                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
-}
+// No v_dot2c_f32_bf16 (or other dot instructions) in MFMA kernels: on gfx950 a dot
+// instruction issues only between the MFMAs of the SIMD's other waves, so it stalls
+// its own wave for the length of the other wave's MFMA stream (measured: 16 dot2c
+// next to an MFMA-bound wave take 252 cycles against 140 alone, while fma, exp, max3,
+// cvt_pk, mul, add and permlane32_swap overlap the MFMAs at full rate).
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, the 64-bit loads of lanes
 // 4r..4r+3 form row r (16 consecutive 16-bit elements) of a 4 x 16 block, and

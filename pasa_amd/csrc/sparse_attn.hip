@@ -35,9 +35,12 @@
 // step: co-resident workgroups on a CU drift into start-time cohorts, each sweeping
 // a different region of key space, and pairing halves the number of cohorts (and so
 // the L2 working set), while each group's phase-2 operands are loaded once for both
-// blocks.  k4_sparse_attn (D = 64) stages tiles through registers and updates the
-// exponentiation max lazily (when a row's max grows by more than 2^8), caught up to
-// the exact phase-1 max before phase 2.
+// blocks.  k4_sparse_attn (D = 64) stages tiles through registers; its online
+// softmax is the same exact one (rescale whenever a row's max rises).
+//
+// Both keep the row sum of P in fp32 (adds, not v_dot2c_f32_bf16: on gfx950 a dot
+// instruction issues only between the MFMAs of the SIMD's other wave, so it stalls
+// its wave behind the partner's MFMA stream).
 //
 // Phase-2 operands (kbar, V^ transposed, Hbar transposed; bf16) are packed per
 // (slice, group) by k4_pack / k4_pack_xor into the exact LDS image K4 copies in.
@@ -222,8 +225,6 @@ __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
 
 // ---- main kernel ------------------------------------------------------------
 
-constexpr float kRescaleThreshold = 0.0f;  // log2 units; 0 = rescale whenever a row max rises
-
 template <int D, int BT>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
 void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -316,8 +317,7 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
     return j;
   };
 
-  float m_use = -INFINITY;   // max used for exponentiation (lags m_true by < 2^8)
-  float m_true = -INFINITY;  // exact running max of the selected scores (log2 units)
+  float m_run = -INFINITY;  // exact running max of the scores (log2 units)
   int blk = next_selected();
   if (blk >= 0) fetch(blk);
   while (blk >= 0) {
@@ -357,11 +357,10 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[mt][r]);
       const float mxc = halves_max(mx) * c;
-      m_true = fmaxf(m_true, mxc);
-      if (__any(mxc > m_use + kRescaleThreshold)) {
-        const float m_new = fmaxf(m_use, mxc);
-        const float alpha = fast_exp2(m_use - m_new);  // 0 on the first step
-        m_use = m_new;
+      if (__any(mxc > m_run)) {
+        const float m_new = fmaxf(m_run, mxc);
+        const float alpha = fast_exp2(m_run - m_new);  // 0 on the first step
+        m_run = m_new;
         l_run *= alpha;
 #pragma unroll
         for (int et = 0; et < D / 32; ++et)
@@ -369,18 +368,20 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
           for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
       }
       bf16x8_t pf[4];
+      float lsum[4] = {0.f, 0.f, 0.f, 0.f};  // fp32 row sum of p, as gpa.py:182-184
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         uint32_t w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p0 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i], c, -m_use));
-          const float p1 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i + 1], c, -m_use));
+          const float p0 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i], c, -m_run));
+          const float p1 = fast_exp2(fmaf(sacc[s4 >> 1][8 * (s4 & 1) + 2 * i + 1], c, -m_run));
           w[i] = pack_bf16x2(p0, p1);
-          l_run = bf16x2_sum(w[i], l_run);
+          lsum[i] += p0 + p1;
         }
         pf[s4] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
       }
+      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         const int rowk = 16 * (kh * 4 + s4);
@@ -395,18 +396,6 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
       }
     }
     blk = nxt;
-  }
-  // Catch the lagging max up to the exact phase-1 max before phase 2.
-  float m_run = m_true;
-  if (m_true != -INFINITY) {
-    const float alpha = fast_exp2(m_use - m_true);
-    l_run *= alpha;
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int et = 0; et < D / 32; ++et)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
-    }
   }
 
   // ---------------- Phase 2: zero- + first-order correction per group --------
@@ -894,7 +883,10 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
     }
+    // The row sum adds the fp32 p (as gpa.py:182-184 sums `score` before its bf16
+    // cast) in four partial sums, then adds the tile's sum to the rescaled l.
     bf16x8_t pf[BT / 16];
+    float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < BT / 16; ++s) {
       uint32_t w[4];
@@ -903,10 +895,11 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         const float p0 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i], c, -m_run));
         const float p1 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i + 1], c, -m_run));
         w[i] = pack_bf16x2(p0, p1);
-        l_run = bf16x2_sum(w[i], l_run);
+        lsum[i] += p0 + p1;
       }
       pf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
     }
+    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     // V_blk is waited for only now, so its load overlaps S and the softmax; the
     // K_{blk+1} loads issued after it may stay in flight.
     if (nxt >= 0)
