@@ -86,11 +86,11 @@ def main() -> int:
         st = ops.block_stats(q, k, v, BT, 32, text_tokens=X)
         pack = ops.pack_phase2(q, st, BT, X)
         e[1].record()
-        sel = ops.select_blocks(st, wl.density, scale)
+        sel = ops.select_blocks(st, wl.density, scale, indices=False)  # K4 reads the bitmask only
         e[2].record()
         ops.sparse_attn_packed(q, k, v, pack, sel, scale, BT, out=out, text_tokens=X)
         e[3].record()
-        last_sel[:] = [sel]
+        last_sel[:] = [sel, st]
 
     log(f"warmup {args.warmup}")
     for i in range(args.warmup):
@@ -272,10 +272,15 @@ def main() -> int:
         # Parity: the selection (index sets per query block, GPU vs oracle on its own fp32
         # scores), then the output against the oracle run on the GPU's selection, so a
         # near-tie resolved differently by score rounding does not mask the attention check.
-        gidx = last_sel[0].idx[:, :h].cpu().reshape(h, NT, -1)
+        # The timed calls skip the index list; the same K3 call with indices writes the
+        # identical bitmask and the top-k order the oracle takes.
+        sel_idx = ops.select_blocks(last_sel[1], wl.density, scale)
+        if not torch.equal(sel_idx.selmask, last_sel[0].selmask):
+            raise RuntimeError("K3 bitmask differs between the calls with and without indices")
+        gidx = sel_idx.idx[:, :h].cpu().reshape(h, NT, -1)
         same = (torch.sort(gidx, -1).values == torch.sort(aux["idx"].reshape(h, NT, -1), -1).values)
         rows_same = same.all(-1).float().mean().item()
-        gsel = last_sel[0].idx[:, :h].cpu()
+        gsel = sel_idx.idx[:, :h].cpu()
         ref_shared = O.pisa_pg_attention(qc, kc2, vc, wl.density, BT, 32, scale, indices=gsel, text_tokens=X)
         # the reference's own precision on the same selection (bf16 P, kc/vc/h_group, output)
         floor_ref = O.pisa_pg_attention(qc, kc2, vc, wl.density, BT, 32, scale, indices=gsel, text_tokens=X,
@@ -369,7 +374,7 @@ def config_step(torch, ops, make_inputs, wl, dev, seed: int, steps: int = 10, wa
         pack = ops.pack_phase2(q, st, BT, X)
         if e is not None:
             e[3].record()
-        sel = ops.select_blocks(st, wl.density, wl.op_scale)
+        sel = ops.select_blocks(st, wl.density, wl.op_scale, indices=False)
         if e is not None:
             e[0].record()
         ops.sparse_attn_packed(q, k, v, pack, sel, wl.op_scale, BT, out=out, text_tokens=X)

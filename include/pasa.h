@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 7
+#define PASA_ABI_VERSION 8
 
 typedef enum {
   PASA_OK = 0,
@@ -136,8 +136,9 @@ size_t pasa_block_stats_workspace_bytes(int64_t bh, int64_t seq_len, int64_t tex
  * scores[I][j] = sum_d qc[I][d] * (scale * kc[j][d])
  *              + (use_cov_bias ? log(hnorm[j] + 1e-6) + (noise ? noise[j] : 0) : 0)
  * idx[I][0..NS) = the NS largest scores of row I, ordered by (score desc, index asc);
- * ties are broken by lowest index; -0.0 and +0.0 compare equal.
- * selmask[I][w] bit b set  <=>  key block 32*w + b is in idx[I]   (uint32 [BH,NT,ceil(NT/32)])
+ * ties are broken by lowest index; -0.0 and +0.0 compare equal.  idx may be NULL: then
+ * only selmask is written (all pasa_sparse_attn reads), and the sort is skipped.
+ * selmask[I][w] bit b set  <=>  key block 32*w + b is among the NS selected   (uint32 [BH,NT,ceil(NT/32)])
  * NS = pasa_num_selected(density, NT).  noise: optional fp32 [BH, NT] (one draw per
  * key block, shared by all query blocks; used only with use_cov_bias).  scores_out:
  * optional fp32 [BH, NT, NT] output; when NULL the workspace holds the scores.
@@ -163,8 +164,8 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
  * in selmask[I], then for each group g of 32 key blocks the zero-order (kc, vc)
  * plus first-order (hgroup) contribution of the blocks of g not selected, merged
  * into the same running max; o = A / (L + Gamma).  The kernel reads the selection
- * from selmask only (idx must be the matching index list, as pasa_select writes
- * it, but is not read): the exact blocks are visited in ascending block order,
+ * from selmask only (idx, the matching index list as pasa_select writes it, is not
+ * read and may be NULL): the exact blocks are visited in ascending block order,
  * which equals the reference's top-k order up to floating-point rounding.
  * gamma_literal = 1 reproduces the reference exactly: Gamma (the zero-order
  * denominator, sum p_j * n_j) is not rescaled when the running max rises;

@@ -258,7 +258,7 @@ int pasa_select(const float* qc, const float* kc, const float* hnorm, const floa
                 double scale, double density, int use_cov_bias, int32_t* idx, uint32_t* selmask,
                 float* scores_out, void* workspace, size_t workspace_bytes, int64_t bh,
                 int64_t num_blocks, int64_t head_dim, void* stream) {
-  if (!qc || !kc || !idx || !selmask) return fail(PASA_ERR_NULL_POINTER, "pasa_select: NULL pointer");
+  if (!qc || !kc || !selmask) return fail(PASA_ERR_NULL_POINTER, "pasa_select: NULL pointer");
   if (use_cov_bias && !hnorm) return fail(PASA_ERR_NULL_POINTER, "pasa_select: hnorm is NULL with use_cov_bias");
   int rc;
   if ((rc = check_select_shape(bh, num_blocks))) return rc;
@@ -284,7 +284,7 @@ int pasa_select(const float* qc, const float* kc, const float* hnorm, const floa
 
 int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint32_t* selmask,
                             int64_t bh, int64_t num_blocks, void* stream) {
-  if (!scores || !idx || !selmask) return fail(PASA_ERR_NULL_POINTER, "pasa_select_from_scores: NULL pointer");
+  if (!scores || !selmask) return fail(PASA_ERR_NULL_POINTER, "pasa_select_from_scores: NULL pointer");
   int rc;
   if ((rc = check_select_shape(bh, num_blocks))) return rc;
   if (ns < 1 || ns > num_blocks) return fail(PASA_ERR_NUM_SELECTED, "ns=%lld not in [1, %lld]", (long long)ns, (long long)num_blocks);
@@ -338,11 +338,13 @@ int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void
                        "pasa_pack_phase2");
 }
 
+// idx is not read (the kernels visit the blocks of selmask), so it may be NULL.
 static int check_attn_args(const void* q, const void* k, const void* v, const int32_t* idx,
                            const uint32_t* selmask, const void* o, double scale, int64_t bh,
                            int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim,
                            int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype) {
-  if (!q || !k || !v || !idx || !selmask || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
+  (void)idx;
+  if (!q || !k || !v || !selmask || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
   if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_sparse_attn: only bf16 inputs are supported");
   int rc;
   if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;

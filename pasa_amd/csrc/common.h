@@ -100,6 +100,16 @@ __device__ __forceinline__ void dma_load16_lds(u32x4_t rsrc, uint32_t lds_addr, 
                : "memory");
 }
 
+// Workgroup barrier without a memory fence, so in-flight direct-to-LDS tile loads
+// are not drained (a fenced __syncthreads would wait for them).  It is used only
+// where this wave's preceding LDS reads have been consumed by MFMAs, i.e. have
+// completed, and where the next LDS writes are direct loads issued after it.
+__device__ __forceinline__ void barrier_lds_reads_done() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads have returned
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");       // no LDS access moves across the barrier
+}
+
 // vmcnt-only wait (expcnt / lgkmcnt left unconstrained), gfx9 s_waitcnt encoding.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -7,93 +7,173 @@
 // is defined against fp32 math).  torch.topk leaves the order of equal scores
 // unspecified; this kernel fixes it: (score desc, index asc), -0.0 == +0.0.
 //
-// Stage 1 (k3_scores): a 64x64-tile fp32 GEMM per (slice, tile) on the fp32 MFMA,
-//   with a fixed d-order, plus the per-key-block log bias.
+// Stage 1 (k3_scores): a 64x128-tile fp32 GEMM on the fp32 MFMA (persistent workgroups,
+//   features double-buffered through LDS), with a fixed d-order, plus the per-key-block
+//   log bias.
 // Stage 2 (k3_topk): one wavefront per row finds the NS-th largest score by a bitwise
 //   search over the orderable 32-bit score (ballot counts, narrowed to one register once
 //   the bucket holding it is small), takes the ties at it by lowest index, emits the
-//   selection bitmask (one bit per key block) from the ballots of the picks, and sorts the
-//   NS selected 64-bit keys (orderable(score) << 32 | ~index) with a bitonic network in
-//   LDS for the indices.
-#include <utility>
-
+//   selection bitmask (one bit per key block) from the ballots of the picks and, when the
+//   caller asks for the index list, sorts the NS selected 64-bit keys
+//   (orderable(score) << 32 | ~index) with a bitonic network.  K4 reads only the bitmask,
+//   so the attention call skips the index list (the reference's indices never leave its
+//   operator either).
 #include "common.h"
 #include "kernels.h"
 
 namespace pasa {
 
-constexpr int kScoreTile = 64;
+constexpr int kScoreTJ = 128;  // key blocks per workgroup tile
+constexpr int kScoreDC = 32;   // features per pipeline stage (one 128-byte row segment)
 
-// One workgroup per 64 x 64 tile of one slice's score matrix, one 32 x 32 sub-tile per
-// wave, on the fp32 MFMA (v_mfma_f32_32x32x2_f32: twice the rate of scalar fp32 FMAs).
-// The dot product over d is taken in a fixed permuted order: in step s the lanes of
-// half-wave hh supply d = hh * D/2 + s, so a lane walks contiguous d and one 16-byte LDS
-// read feeds four MFMAs.  Rows are staged in LDS as fp32 with a 4-float pad; kc * scale is
+// Byte offset, inside an LDS stage block of 128-byte rows, of 16-byte chunk c (of 8) of
+// tile row r: the chunk is stored at c ^ ((r >> 1) & 7), so the float4 reads of any 16
+// consecutive rows at one logical chunk touch 16 distinct 16-byte bank groups.
+__host__ __device__ __forceinline__ constexpr int score_chunk_byte(int r, int c) {
+  return r * 128 + ((c ^ ((r >> 1) & 7)) << 4);
+}
+
+// Each workgroup computes 64 x 128 tiles of the score matrices (query blocks x key
+// blocks), one after another (tile blockIdx.x, then + gridDim.x, ...; the grid is sized
+// to three workgroups per CU), so a tile's stores drain while the next tile is
+// multiplied.  Four waves each compute 32 query rows x 64 key columns as two 32 x 32
+// sub-tiles on the fp32 MFMA (v_mfma_f32_32x32x2_f32).  The features are consumed in
+// stages of 32, double-buffered in LDS (48 KB): the qc and kc rows of the next stage
+// (the next tile's first stage after a tile's last) stream in by direct-to-LDS loads
+// (rows past NT read as zero) while the current stage is multiplied.  The dot product
+// over d is taken in a fixed order: within stage c, the half-wave hh of a lane supplies
+// d = 32c + 16hh + s in step s, so one float4 read feeds four MFMAs.  kc * scale is
 // rounded to fp32 before the product, as the reference computes it.
 template <int D>
 __global__ __launch_bounds__(256) void k3_scores(const float* __restrict__ qc,
                                                  const float* __restrict__ kc,
                                                  const float* __restrict__ hnorm,
                                                  const float* __restrict__ noise, float scale,
-                                                 int use_cov_bias, float* __restrict__ scores, int NT) {
-  constexpr int RS = D + 4;  // padded row stride (floats)
-  __shared__ __attribute__((aligned(16))) float As[kScoreTile * RS];
-  __shared__ __attribute__((aligned(16))) float Bs[kScoreTile * RS];
-  const int bh = blockIdx.z;
-  const int i0 = blockIdx.y * kScoreTile;
-  const int j0 = blockIdx.x * kScoreTile;
+                                                 int use_cov_bias, float* __restrict__ scores, int NT,
+                                                 int ntj, int tiles_per_slice, int ntiles) {
+  constexpr int TI = 64;
+  constexpr int NC = D / kScoreDC;              // stages per tile
+  constexpr int A_BYTES = TI * 128;             // 64 query rows x 32 floats
+  constexpr int B_BYTES = kScoreTJ * 128;       // 128 key rows x 32 floats
+  constexpr int STAGE = A_BYTES + B_BYTES;      // 24 KB: 24 direct loads of 1 KB
+  constexpr int LOADS = STAGE / 1024 / 4;       // per wave per stage
+  static_assert(D % kScoreDC == 0 && STAGE % 4096 == 0, "stage split");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * STAGE];
   const int tid = threadIdx.x;
-  const float* qb = qc + (int64_t)bh * NT * D;
-  const float* kb = kc + (int64_t)bh * NT * D;
-  // Stage 64 rows of qc and of scale * kc, 16 bytes per thread per step.
-  constexpr int C4 = D / 4;  // float4 per row
-  for (int u = tid; u < kScoreTile * C4; u += 256) {
-    const int r = u / C4;
-    const int c4 = u - r * C4;
-    const int gi = i0 + r;
-    const int gj = j0 + r;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-    if (gi < NT) a = *reinterpret_cast<const float4*>(qb + (int64_t)gi * D + 4 * c4);
-    if (gj < NT) {
-      b = *reinterpret_cast<const float4*>(kb + (int64_t)gj * D + 4 * c4);
-      b = make_float4(scale * b.x, scale * b.y, scale * b.z, scale * b.w);  // kc * scale first
-    }
-    *reinterpret_cast<float4*>(As + r * RS + 4 * c4) = a;
-    *reinterpret_cast<float4*>(Bs + r * RS + 4 * c4) = b;
-  }
-  __syncthreads();
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t slice_bytes = (uint32_t)NT * D * 4u;
+  const uint32_t lds0 = lds_addr(lds);
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-  const int ar = (wave >> 1) * 32 + l32;  // row of A (query block) this lane supplies
-  const int br = (wave & 1) * 32 + l32;   // row of B (key block)
-  const float* ap = As + ar * RS + hh * (D / 2);
-  const float* bp = Bs + br * RS + hh * (D / 2);
-  f32x16_t acc;
+  const int ar = (wave >> 1) * 32 + l32;  // query row of the tile this lane supplies
+  const int br0 = (wave & 1) * 64 + l32;  // key rows of its two sub-tiles: br0, br0 + 32
+
+  // Direct load n of this wave fills 1 KB piece p = 4n + wave of a stage: pieces 0-7
+  // hold query rows 8p .. 8p + 7, pieces 8-23 key rows 8(p - 8) .. ; lane L writes physical
+  // chunk L & 7 of row 8p' + L/8, which holds logical chunk (L & 7) ^ ((row >> 1) & 7).
+  uint32_t roff[LOADS];  // byte offset of the lane's chunk within its tile's row block
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-#pragma unroll
-  for (int s4 = 0; s4 < D / 8; ++s4) {
-    const float4 a = *reinterpret_cast<const float4*>(ap + 4 * s4);
-    const float4 b = *reinterpret_cast<const float4*>(bp + 4 * s4);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+  for (int n = 0; n < LOADS; ++n) {
+    const int p = 4 * n + wave;
+    const int row = (p < TI / 8 ? p : p - TI / 8) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    roff[n] = (uint32_t)row * (uint32_t)(D * 4) + (uint32_t)(c * 16);
   }
-  // C: row (query block) 8(r>>2) + 4hh + (r&3) of the wave's sub-tile, column (key block) l32.
-  const int gj = j0 + (wave & 1) * 32 + l32;
-  if (gj >= NT) return;
-  float bias = 0.f;
-  if (use_cov_bias) {
-    bias = logf(hnorm[(int64_t)bh * NT + gj] + 1e-6f);
-    if (noise) bias = bias + noise[(int64_t)bh * NT + gj];
-  }
+  struct Tile {
+    int bh, i0, j0;
+  };
+  auto tile_of = [&](int t) -> Tile {
+    const int bh = t / tiles_per_slice;
+    const int r = t - bh * tiles_per_slice;
+    const int ti = r / ntj;
+    return Tile{bh, ti * TI, (r - ti * ntj) * kScoreTJ};
+  };
+  auto load_stage = [&](const Tile& tl, int st, int buf) {
+    const u32x4_t qd = make_rsrc_words(qc + (int64_t)tl.bh * NT * D, slice_bytes);
+    const u32x4_t kd = make_rsrc_words(kc + (int64_t)tl.bh * NT * D, slice_bytes);
+    const uint32_t qrow = (uint32_t)tl.i0 * (uint32_t)(D * 4) + (uint32_t)(st * kScoreDC * 4);
+    const uint32_t krow = (uint32_t)tl.j0 * (uint32_t)(D * 4) + (uint32_t)(st * kScoreDC * 4);
+    const uint32_t base = lds0 + buf * STAGE;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int gi = i0 + (wave >> 1) * 32 + mfma32_row(r, hh);
-    if (gi < NT) scores[((int64_t)bh * NT + gi) * NT + gj] = acc[r] + bias;
+    for (int n = 0; n < LOADS; ++n) {
+      const int p = 4 * n + wave;
+      if (p < TI / 8)
+        dma_load16_lds(qd, base + p * 1024, roff[n] + qrow, 0u);
+      else
+        dma_load16_lds(kd, base + p * 1024, roff[n] + krow, 0u);
+    }
+  };
+
+  int t = blockIdx.x;
+  if (t >= ntiles) return;
+  Tile cur = tile_of(t);
+  int buf = 0;
+  load_stage(cur, 0, buf);
+  while (true) {
+    const int tn = t + (int)gridDim.x;
+    const bool more = tn < ntiles;
+    const Tile nxt = more ? tile_of(tn) : cur;
+    f32x16_t acc0, acc1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc0[r] = 0.f;
+      acc1[r] = 0.f;
+    }
+#pragma unroll
+    for (int st = 0; st < NC; ++st) {
+      // Prefetch the next stage (the next tile's first after this tile's last).
+      const bool pre = st + 1 < NC || more;
+      if (pre) {
+        load_stage(st + 1 < NC ? cur : nxt, st + 1 < NC ? st + 1 : 0, buf ^ 1);
+        wait_vmcnt<LOADS>();  // this wave's part of this stage landed (the next may be in flight)
+      } else {
+        wait_vmcnt<0>();
+      }
+      barrier_lds_reads_done();  // ... and every wave's
+      const unsigned char* sa = lds + buf * STAGE;
+      const unsigned char* sb = sa + A_BYTES;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int c = hh * 4 + s4;  // logical chunk: features 16hh + 4s4 .. + 3 of the stage
+        const float4 a = *reinterpret_cast<const float4*>(sa + score_chunk_byte(ar, c));
+        float4 b0 = *reinterpret_cast<const float4*>(sb + score_chunk_byte(br0, c));
+        float4 b1 = *reinterpret_cast<const float4*>(sb + score_chunk_byte(br0 + 32, c));
+        b0 = make_float4(scale * b0.x, scale * b0.y, scale * b0.z, scale * b0.w);  // kc * scale first
+        b1 = make_float4(scale * b1.x, scale * b1.y, scale * b1.z, scale * b1.w);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0.x, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b1.x, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b0.y, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1.y, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b0.z, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b1.z, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b0.w, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b1.w, acc1, 0, 0, 0);
+      }
+      barrier_lds_reads_done();  // every wave is done with this stage's buffer
+      buf ^= 1;
+    }
+    // C: row (query block) 8(r>>2) + 4hh + (r&3) of a sub-tile, column (key block) l32.
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int gj = cur.j0 + br0 + 32 * s2;
+      if (gj < NT) {
+        float bias = 0.f;
+        if (use_cov_bias) {
+          bias = logf(hnorm[(int64_t)cur.bh * NT + gj] + 1e-6f);
+          if (noise) bias = bias + noise[(int64_t)cur.bh * NT + gj];
+        }
+        const f32x16_t& acc = s2 ? acc1 : acc0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int gi = cur.i0 + (wave >> 1) * 32 + mfma32_row(r, hh);
+          if (gi < NT) scores[((int64_t)cur.bh * NT + gi) * NT + gj] = acc[r] + bias;
+        }
+      }
+    }
+    if (!more) break;
+    t = tn;
+    cur = nxt;
   }
 }
 
@@ -144,21 +224,20 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// x with lane L replaced by the wave-uniform v (v_writelane_b32).
-template <int L>
-__device__ __forceinline__ uint32_t write_lane(uint32_t x, uint32_t v) {
-  asm("v_writelane_b32 %0, %1, %2" : "+v"(x) : "s"(__builtin_amdgcn_readfirstlane(v)), "n"(L));
-  return x;
-}
-
 // Blocks 64 i .. 64 i + 63 are mask words 2 i (lanes 0-31 of pbs[i]) and 2 i + 1; word w
-// goes to lane w % 64 of mw[w / 64].
-template <int... I>
-__device__ __forceinline__ void set_mask_words(std::integer_sequence<int, I...>, const uint64_t* pbs,
-                                               uint32_t (&mw)[2]) {
-  ((mw[(2 * I) / 64] = write_lane<(2 * I) % 64>(mw[(2 * I) / 64], (uint32_t)pbs[I]),
-    mw[(2 * I + 1) / 64] = write_lane<(2 * I + 1) % 64>(mw[(2 * I + 1) / 64], (uint32_t)(pbs[I] >> 32))),
-   ...);
+// goes to lane w % 64 of mw[w / 64].  Each lane selects its words with compares (the
+// compiler schedules these; an inline-asm v_writelane right after the VALU write of its
+// register wrote a stale word 0 when nothing else separated them).
+template <int KPL>
+__device__ __forceinline__ void set_mask_words(const uint64_t (&pbs)[KPL], int lane, uint32_t (&mw)[2]) {
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int w0 = 2 * i;
+    const uint32_t lo = (uint32_t)pbs[i];
+    const uint32_t hi = (uint32_t)(pbs[i] >> 32);
+    if (lane == (w0 & 63)) mw[w0 >> 6] = lo;
+    if (lane == ((w0 + 1) & 63)) mw[(w0 + 1) >> 6] = hi;
+  }
 }
 
 // The 64-bit value of lane ^ m.
@@ -234,11 +313,11 @@ __device__ __forceinline__ void sort_and_store(const uint64_t* sel, int NS, int 
 }
 
 // The picks of a row: every score above T and, when RANK, of the scores equal to T the
-// `need` with the lowest indices (without RANK every tie is taken).  The picked keys go to
-// sel in index order (a lane that does not pick writes its own slot past NSP instead, so
-// the store needs no branch); mw receives the selection mask, word w in lane w % 64 of
-// mw[w / 64].
-template <int KPL, bool RANK>
+// `need` with the lowest indices (without RANK every tie is taken).  With KEYS, the picked
+// keys go to sel in index order (a lane that does not pick writes its own slot past NSP
+// instead, so the store needs no branch); mw receives the selection mask, word w in lane
+// w % 64 of mw[w / 64].
+template <int KPL, bool RANK, bool KEYS>
 __device__ __forceinline__ void pick_row(const uint32_t (&ok)[KPL], uint32_t T, uint32_t need, int NSP,
                                          int lane, uint64_t* sel, uint32_t (&mw)[2]) {
   uint32_t taken = 0u;  // ties at T taken so far (in index order)
@@ -256,12 +335,14 @@ __device__ __forceinline__ void pick_row(const uint32_t (&ok)[KPL], uint32_t T, 
       pick = ok[i] >= T;  // T >= 1, so a missing key (0) is never picked
     }
     const uint64_t pb = ballot(pick);
-    const uint32_t pos = pick ? base + lanes_below(pb) : (uint32_t)(NSP + lane);
-    sel[pos] = ((uint64_t)ok[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i * 64 + lane));
-    base += (uint32_t)__popcll(pb);
+    if constexpr (KEYS) {
+      const uint32_t pos = pick ? base + lanes_below(pb) : (uint32_t)(NSP + lane);
+      sel[pos] = ((uint64_t)ok[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i * 64 + lane));
+      base += (uint32_t)__popcll(pb);
+    }
     pbs[i] = pb;
   }
-  set_mask_words(std::make_integer_sequence<int, KPL>(), pbs, mw);
+  set_mask_words<KPL>(pbs, lane, mw);
 }
 
 // Slots counted in the VALU per search step (the rest by ballots).
@@ -279,7 +360,8 @@ constexpr int kValuSlots = KPL / 3;
 // of the picks (two 32-block words per register); the NS picked keys
 // (score << 32 | ~index) are packed into LDS in index order and sorted descending in
 // registers (NS <= 256) or in LDS.  Dynamic LDS: (NSP + 64) * 8 bytes (NSP = pow2 >= NS).
-template <int KPL>
+// Without IDX only the bitmask is written (what K4 reads): no keys, no sort.
+template <int KPL, bool IDX>
 __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, int NT, int NS, int NSP,
                                               int NW, int32_t* __restrict__ idx,
                                               uint32_t* __restrict__ selmask) {
@@ -364,12 +446,13 @@ __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, 
   const uint32_t need = (uint32_t)NS - hi;
   uint32_t mw[2] = {0u, 0u};
   if (lo - hi == need)
-    pick_row<KPL, false>(ok, prefix, need, NSP, lane, sel, mw);
+    pick_row<KPL, false, IDX>(ok, prefix, need, NSP, lane, sel, mw);
   else
-    pick_row<KPL, true>(ok, prefix, need, NSP, lane, sel, mw);
+    pick_row<KPL, true, IDX>(ok, prefix, need, NSP, lane, sel, mw);
   uint32_t* mrow = selmask + ((int64_t)bh * NT + row) * NW;
   if (lane < NW) mrow[lane] = mw[0];
   if (64 + lane < NW) mrow[64 + lane] = mw[1];
+  if constexpr (!IDX) return;
   __syncthreads();
 
   int32_t* irow = idx + ((int64_t)bh * NT + row) * NS;
@@ -390,13 +473,19 @@ __global__ __launch_bounds__(64) void k3_topk(const float* __restrict__ scores, 
 hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,
                          float scale, int use_cov_bias, float* scores, int bh, int NT, int D,
                          hipStream_t stream) {
-  dim3 grid((NT + kScoreTile - 1) / kScoreTile, (NT + kScoreTile - 1) / kScoreTile, bh);
+  const int nti = (NT + 63) / 64;
+  const int ntj = (NT + kScoreTJ - 1) / kScoreTJ;
+  const int ntiles = bh * nti * ntj;
+  // Three workgroups per CU of the MI355X (256 CUs); each loops over its tiles, so any
+  // grid size is correct.
+  constexpr int kResident = 3 * 256;
+  const int grid = ntiles < kResident ? ntiles : kResident;
   if (D == 128)
-    hipLaunchKernelGGL(k3_scores<128>, grid, dim3(256), 0, stream, qc, kc, hnorm, noise, scale, use_cov_bias,
-                       scores, NT);
+    hipLaunchKernelGGL((k3_scores<128>), dim3(grid), dim3(256), 0, stream, qc, kc, hnorm, noise, scale, use_cov_bias,
+                       scores, NT, ntj, nti * ntj, ntiles);
   else if (D == 64)
-    hipLaunchKernelGGL(k3_scores<64>, grid, dim3(256), 0, stream, qc, kc, hnorm, noise, scale, use_cov_bias,
-                       scores, NT);
+    hipLaunchKernelGGL((k3_scores<64>), dim3(grid), dim3(256), 0, stream, qc, kc, hnorm, noise, scale, use_cov_bias,
+                       scores, NT, ntj, nti * ntj, ntiles);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -409,10 +498,13 @@ hipError_t launch_topk(const float* scores, int bh, int NT, int NS, int32_t* idx
   if (NSP < 2) NSP = 2;
   const int NW = (NT + 31) / 32;
   dim3 grid(NT, bh);
-  const size_t lds = (size_t)(NSP + 64) * sizeof(uint64_t);
-#define PASA_TOPK(K) \
-  case K:          \
-    hipLaunchKernelGGL((k3_topk<K>), grid, dim3(64), lds, stream, scores, NT, NS, NSP, NW, idx, selmask); \
+  const size_t lds = idx ? (size_t)(NSP + 64) * sizeof(uint64_t) : 0;
+#define PASA_TOPK(K)                                                                                         \
+  case K:                                                                                                    \
+    if (idx)                                                                                                 \
+      hipLaunchKernelGGL((k3_topk<K, true>), grid, dim3(64), lds, stream, scores, NT, NS, NSP, NW, idx, selmask); \
+    else                                                                                                     \
+      hipLaunchKernelGGL((k3_topk<K, false>), grid, dim3(64), lds, stream, scores, NT, NS, NSP, NW, idx, selmask); \
     break;
   // Registers per lane: ceil(NT / 64) rounded up to a multiple of 4.
   switch (4 * ((NT + 255) / 256)) {

@@ -130,25 +130,29 @@ def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: i
 
 @dataclass
 class Selection:
-    """Outputs of K3.  idx int32 [B,H,NT,NS] (score desc, index asc); selmask int32 view of
-    uint32 words [B,H,NT,ceil(NT/32)]; scores fp32 [B,H,NT,NT] when requested."""
-    idx: torch.Tensor
+    """Outputs of K3.  idx int32 [B,H,NT,NS] (score desc, index asc), or None when not
+    requested (K4 reads only selmask); selmask int32 view of uint32 words
+    [B,H,NT,ceil(NT/32)]; scores fp32 [B,H,NT,NT] when requested."""
+    idx: Optional[torch.Tensor]
     selmask: torch.Tensor
     scores: Optional[torch.Tensor]
     ns: int
 
 
 def select_blocks(stats: BlockStats, density: float, scale: float, use_cov_bias: bool = True,
-                  noise: Optional[torch.Tensor] = None, return_scores: bool = False) -> Selection:
+                  noise: Optional[torch.Tensor] = None, return_scores: bool = False,
+                  indices: bool = True) -> Selection:
     """Covariance-aware top-k of key blocks per query block (reference :365-375).
 
     ``noise``: optional fp32 [B,H,NT], one draw per key block (the reference's
-    ``use_random``), added to the log bias only when ``use_cov_bias``."""
+    ``use_random``), added to the log bias only when ``use_cov_bias``.
+    ``indices=False`` skips the index list (Selection.idx is None): the bitmask alone
+    drives the attention kernel, and the per-row sort is not run."""
     qc, kc, hnorm = stats.qc, stats.kc, stats.hnorm
     _check_device(qc, kc, hnorm)
     B, H, NT, D = qc.shape
     ns = num_selected(density, NT)
-    idx = torch.empty(B, H, NT, ns, device=qc.device, dtype=torch.int32)
+    idx = torch.empty(B, H, NT, ns, device=qc.device, dtype=torch.int32) if indices else None
     nw = (NT + 31) // 32
     selmask = torch.empty(B, H, NT, nw, device=qc.device, dtype=torch.int32)
     if noise is not None:
@@ -157,7 +161,7 @@ def select_blocks(stats: BlockStats, density: float, scale: float, use_cov_bias:
             raise ValueError("noise must be fp32 with B*H*NT elements")
     scores = torch.empty(B, H, NT, NT, device=qc.device, dtype=torch.float32)
     _lib.call("pasa_select", qc.data_ptr(), kc.data_ptr(), hnorm.data_ptr(), _ptr(noise),
-              float(scale), float(density), int(bool(use_cov_bias)), idx.data_ptr(),
+              float(scale), float(density), int(bool(use_cov_bias)), _ptr(idx),
               selmask.data_ptr(), scores.data_ptr(), None, 0, B * H, NT, D, _stream(qc))
     return Selection(idx, selmask, scores if return_scores else None, ns)
 
@@ -209,10 +213,13 @@ def _check_selection(sel: Selection, q: torch.Tensor, block_size: int, text_toke
     B, H, T, _ = q.shape
     NT = math.ceil((T - int(text_tokens)) / block_size)
     nw = (NT + 31) // 32
-    _check_device(sel.idx, sel.selmask)
+    _check_device(sel.selmask)
     if sel.selmask.dtype not in (torch.int32, torch.uint32) or tuple(sel.selmask.shape) != (B, H, NT, nw):
         raise ValueError(f"selmask must be int32 [{B}, {H}, {NT}, {nw}] for block_size {block_size}, "
                          f"got {sel.selmask.dtype} {tuple(sel.selmask.shape)}")
+    if sel.idx is None:
+        return
+    _check_device(sel.idx)
     if sel.idx.dtype != torch.int32 or tuple(sel.idx.shape[:3]) != (B, H, NT) or sel.idx.dim() != 4:
         raise ValueError(f"idx must be int32 [{B}, {H}, {NT}, ns] for block_size {block_size}, "
                          f"got {sel.idx.dtype} {tuple(sel.idx.shape)}")
@@ -234,7 +241,7 @@ def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: 
         raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     _check_selection(sel, q, block_size, text_tokens)
     o = _check_out(v, out)
-    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(), pack.numel(), sel.idx.data_ptr(),
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(), pack.numel(), _ptr(sel.idx),
             sel.selmask.data_ptr(), o.data_ptr(), float(scale), B * H, T, int(text_tokens),
             int(text_tokens if text_valid is None else text_valid), D, block_size, GROUP_SIZE, sel.ns,
             int(gamma == "literal"))
@@ -276,7 +283,7 @@ def sparse_attn_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats
     _check_selection(sel, q, block_size, text_tokens)
     o = _check_out(v, out)
     _lib.call("pasa_sparse_attn_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), stats.kc.data_ptr(),
-              stats.vc.data_ptr(), stats.hgroup.data_ptr(), sel.idx.data_ptr(), sel.selmask.data_ptr(),
+              stats.vc.data_ptr(), stats.hgroup.data_ptr(), _ptr(sel.idx), sel.selmask.data_ptr(),
               o.data_ptr(), float(scale), B * H, T, int(text_tokens),
               int(text_tokens if text_valid is None else text_valid), D, block_size, GROUP_SIZE, sel.ns,
               int(gamma == "literal"), _DTYPES.get(q.dtype, -1), _stream(q))
@@ -353,7 +360,9 @@ def pisa_pg_attention(
     stats = block_stats(q, k, v, block_size, group_size, text_tokens, placement)
     if use_random and use_cov_bias and noise is None:
         noise = torch.randn(B, H, NT, device=q.device, dtype=torch.float32)
-    sel = select_blocks(stats, density, scale, use_cov_bias, noise if use_cov_bias else None)
+    # The operator returns o only, and K4 reads the selection bitmask, so the index
+    # list (the reference's topk order) is not built.
+    sel = select_blocks(stats, density, scale, use_cov_bias, noise if use_cov_bias else None, indices=False)
     if verbose:
         print(f"NT={NT}, N_GROUPS={stats.hgroup.shape[2]}, GROUP_SIZE={group_size}")
         print(f"top_k={sel.ns}, density={density}")

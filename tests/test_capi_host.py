@@ -120,7 +120,8 @@ def select(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(qc=None), -1), (dict(idx=None), -1), (dict(hn=None), -1), (dict(nt=0), -2),
+    (dict(qc=None), -1), (dict(mask=None), -1), (dict(idx=None, mask=None), -1), (dict(hn=None), -1),
+    (dict(idx=None, nt=0), -2), (dict(nt=0), -2),
     (dict(nt=5000), -13), (dict(D=32), -3), (dict(scale=float("inf")), -9),
     (dict(density=float("nan")), -9), (dict(scores=None), -8),
     (dict(scores=None, ws=FAKE, wsb=100), -8), (dict(bh=1 << 20), -6),
@@ -133,6 +134,8 @@ def test_select_validation(lib, kw, code):
 def test_select_from_scores_validation(lib):
     f = lib.pasa_select_from_scores
     assert f(None, 1, FAKE, FAKE, 1, 10, None) == -1
+    assert f(FAKE, 1, FAKE, None, 1, 10, None) == -1  # selmask is required
+    assert f(FAKE, 0, None, FAKE, 1, 10, None) == -5  # idx is optional: the shape checks still run
     assert f(FAKE, 0, FAKE, FAKE, 1, 10, None) == -5
     assert f(FAKE, 11, FAKE, FAKE, 1, 10, None) == -5
     assert f(FAKE, 3, FAKE, FAKE, 1, 4097, None) == -13
@@ -151,7 +154,8 @@ def attn(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(o=None), -1), (dict(idx=None), -1), (dict(dtype=2), -7), (dict(D=256), -3),
+    (dict(o=None), -1), (dict(mask=None), -1), (dict(idx=None, mask=None), -1), (dict(idx=None, D=256), -3),
+    (dict(dtype=2), -7), (dict(D=256), -3),
     (dict(BT=256), -4), (dict(G=16), -12), (dict(ns=0), -5), (dict(ns=9), -5),
     (dict(scale=0.0), -9), (dict(scale=-1.0), -9), (dict(scale=float("nan")), -9),
     (dict(lit=2), -9), (dict(ws=None), -8), (dict(wsb=10), -8), (dict(T=0), -2),

@@ -228,6 +228,29 @@ def test_select(device, heads, grid, D, BT, density, use_noise):
     np.testing.assert_array_equal(sel.idx.cpu().numpy(), want.numpy())
 
 
+@pytest.mark.parametrize("heads,grid,BT,density", [
+    (2, (4, 16, 16), 64, 0.25),       # NS 4: one register of keys
+    (1, (21, 45, 80), 64, 0.10),      # c2 at block 64: NT 1182, NS 118
+    (1, (33, 45, 80), 128, 0.10),     # c3 video rows: NT 929, NS 92
+])
+def test_select_without_indices(device, heads, grid, BT, density):
+    """idx = NULL skips the index list: the bitmask is the one the full call writes, and
+    K4 computes the same output bit for bit from it."""
+    D = 128
+    wl, (q, k, v) = bf16_inputs(heads, grid, D, BT)
+    say(f"[K3] select without indices heads={heads} T={wl.seq_len} BT={BT}")
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    st = ops.block_stats(qd, kd, vd, BT, 32)
+    scale = D ** -0.5
+    full = ops.select_blocks(st, density, scale)
+    bare = ops.select_blocks(st, density, scale, indices=False)
+    assert bare.idx is None
+    assert torch.equal(bare.selmask, full.selmask)
+    o_full = ops.sparse_attn(qd, kd, vd, st, full, scale, BT)
+    o_bare = ops.sparse_attn(qd, kd, vd, st, bare, scale, BT)
+    assert torch.equal(o_full.view(torch.int16), o_bare.view(torch.int16))
+
+
 # ---------------------------------------------------------------- K4 --------
 
 ATTN_CASES = [
