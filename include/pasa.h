@@ -243,16 +243,21 @@ typedef struct {
   int64_t heads;                   /* slice s is head s % heads                            */
 } pasa_placement_t;
 
-/* pasa_block_stats and pasa_sparse_attn_packed on frame-major q, k, v (o written
- * frame-major): the result equals permuting q, k, v to token-major (pasa_permute),
- * running the unplaced entry points and permuting o back, without the three extra
- * passes over HBM.  head_dim 128, block_size 128; arguments otherwise as for the
- * unplaced entry points (pasa_block_stats_placed's workspace as pasa_block_stats_ws's:
- * with the same workspace the group moments equal the unplaced call's bit for bit).
+/* The placement folded into K2 and K4.  pasa_block_stats_placed reads frame-major
+ * q, k, v once: it computes the statistics of their token-major view and writes that
+ * view to q_tm, k_tm, v_tm (device bf16 [BH, seq_len, head_dim], text rows copied in
+ * place) in the same pass.  pasa_sparse_attn_packed_placed takes those token-major
+ * copies as q, k, v and stores o frame-major.  Together they equal pasa_permute ->
+ * pasa_block_stats -> ... -> pasa_sparse_attn_packed -> inverse pasa_permute bit for
+ * bit, without the permutation's separate read of q, k, v and its second pass over o.
+ * head_dim 128, block_size 128; arguments otherwise as for the unplaced entry points
+ * (pasa_block_stats_placed's workspace as pasa_block_stats_ws's: with the same
+ * workspace the group moments equal the unplaced call's bit for bit).
  * Replaces: hunyuan_sparse_head_placement / hunyuan_hidden_states_placement around the
  * attention call (svg/models/hyvideo/placement.py:124-153, :360-387;
  * svg/models/hyvideo/attention.py:412-446). */
 int pasa_block_stats_placed(const void* q, const void* k, const void* v,
+                            void* q_tm, void* k_tm, void* v_tm,
                             float* qc, float* kc, float* vc, float* hnorm, float* hgroup,
                             int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim,
                             int64_t block_size, int64_t group_size,

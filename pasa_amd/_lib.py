@@ -73,8 +73,8 @@ SIGNATURES = {
     "pasa_pack_phase2": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "pasa_sparse_attn_packed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
-    "pasa_block_stats_placed": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
-                                       _i64, _pl, _int, _vp, _sz, _vp]),
+    "pasa_block_stats_placed": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                       _i64, _i64, _i64, _pl, _int, _vp, _sz, _vp]),
     "pasa_sparse_attn_packed_placed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                               _i64, _i64, _i64, _i64, _i64, _int, _pl, _int, _vp]),
     "pasa_dense_attn": (_int, [_vp, _vp, _vp, _vp, _dbl, _i64, _i64, _i64, _i64, _i64, _int, _vp]),

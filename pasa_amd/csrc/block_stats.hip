@@ -217,14 +217,18 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 // chunk c of row r at c ^ 4(r & 3)); Q rows go to registers.  Block j+1's loads are in
 // flight while block j is reduced.  H_j = K^T V reads both MFMA operands with the
 // transposing ds_read_b64_tr_b16 (K^T as A, V as B; the same token order in both).
-// PERM: q, k, v are frame-major; the statistics are those of their token-major view (rm).
+// PERM: q, k, v are frame-major; the statistics are those of their token-major view (rm),
+// and the token-major view itself is written to qt, kt, vt: each row of a block goes out
+// from the registers (Q) and LDS tiles (K, V) the column sums read it from, and the
+// workgroup of group 0 copies the text rows [T, Tslice), which stay in place.
 // BT 128 (two 64 KB buffer pairs: one workgroup per CU) or 64 (two per CU).
 template <int BT, bool PERM>
 __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, float* __restrict__ qc, float* __restrict__ kc,
     float* __restrict__ vc, float* __restrict__ hnorm, float* __restrict__ hgroup, int T, int Tslice,
-    int NT, int G, RowMap rm, int split, float* __restrict__ partials) {
+    int NT, int G, RowMap rm, int split, float* __restrict__ partials, uint16_t* __restrict__ qt,
+    uint16_t* __restrict__ kt, uint16_t* __restrict__ vt) {
   constexpr int D = 128;
   constexpr int TILE = BT * 256;
   __shared__ __attribute__((aligned(1024))) unsigned char Kb[2 * TILE];
@@ -346,14 +350,22 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     for (int p = 0; p < BT / 16; ++p) {
       const int r = 16 * p + prow;
       const int off = r * 256 + ((pc ^ (4 * (r & 3))) << 4);
+      const uint4 kx = lds_ld<uint4>(Kt, off);
+      const uint4 vx = lds_ld<uint4>(Vt, off);
+      if (PERM && j * BT + r < T) {  // the token-major copies (rows past T hold text)
+        const int64_t e = slice + (int64_t)(j * BT + r) * D + pc * 8;
+        *reinterpret_cast<uint4*>(qt + e) = qv[p];
+        *reinterpret_cast<uint4*>(kt + e) = kx;
+        *reinterpret_cast<uint4*>(vt + e) = vx;
+      }
       float f[8];
       unpack8(qv[p], f);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ps[0][i] += f[i];
-      unpack8(lds_ld<uint4>(Kt, off), f);
+      unpack8(kx, f);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ps[1][i] += f[i];
-      unpack8(lds_ld<uint4>(Vt, off), f);
+      unpack8(vx, f);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ps[2][i] += f[i];
     }
@@ -431,6 +443,16 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     for (int p = 0; p < BT / 16; ++p) qv[p] = qn[p];
   }
 
+  if (PERM && g == 0 && part == 0) {  // the text rows, in place in both layouts
+    const int64_t n16 = (int64_t)(Tslice - T) * (D / 8);
+    const int64_t base = slice + (int64_t)T * D;
+    for (int64_t i = tid; i < n16; i += 256) {
+      *reinterpret_cast<uint4*>(qt + base + 8 * i) = *reinterpret_cast<const uint4*>(q + base + 8 * i);
+      *reinterpret_cast<uint4*>(kt + base + 8 * i) = *reinterpret_cast<const uint4*>(k + base + 8 * i);
+      *reinterpret_cast<uint4*>(vt + base + 8 * i) = *reinterpret_cast<const uint4*>(v + base + 8 * i);
+    }
+  }
+
   // Unsplit: the group mean (the reference zero-pads the last group to G blocks).
   // Split: this part's raw sum, reduced in a fixed order by k2_group_reduce.
   const int NG = (NT + G - 1) / G;
@@ -487,7 +509,8 @@ int block_stats_split(int bh, int T, int D, int BT, int G) {
 
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
-                              int BT, int G, const RowMap* rm, float* partials, int split, hipStream_t stream) {
+                              int BT, int G, const RowMap* rm, void* const* tm_copies, float* partials, int split,
+                              hipStream_t stream) {
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + G - 1) / G;
   if (split < 1 || split > G || (split > 1 && (partials == nullptr || D != 128 || (BT != 128 && BT != 64))))
@@ -497,15 +520,16 @@ hipError_t launch_block_stats(const void* q, const void* k, const void* v, float
   auto b = (const uint16_t*)k;
   auto c = (const uint16_t*)v;
   if (rm != nullptr) {  // token-major view of frame-major slices: D = 128, BT = 128 only
-    if (D != 128 || BT != 128) return hipErrorInvalidValue;
+    if (D != 128 || BT != 128 || tm_copies == nullptr) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k2_block_stats_dma<128, true>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, *rm, split, partials);
+                       hgroup, T, Tslice, NT, G, *rm, split, partials, (uint16_t*)tm_copies[0],
+                       (uint16_t*)tm_copies[1], (uint16_t*)tm_copies[2]);
   } else if (D == 128 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats_dma<128, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials);
+                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials, nullptr, nullptr, nullptr);
   else if (D == 128 && BT == 64)
     hipLaunchKernelGGL((k2_block_stats_dma<64, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials);
+                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials, nullptr, nullptr, nullptr);
   else if (D == 64 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats<64, 128>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
                        hnorm, hgroup, T, Tslice, NT, G);

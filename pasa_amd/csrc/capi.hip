@@ -156,7 +156,8 @@ int pasa_permute(const void* src0, const void* src1, const void* src2, void* dst
 static int block_stats_impl(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
                             float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t head_dim, int64_t block_size, int64_t group_size, int dtype,
-                            const pasa::RowMap* rm, void* workspace, size_t workspace_bytes, void* stream) {
+                            const pasa::RowMap* rm, void* const* tm_copies, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
   if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_block_stats: only bf16 inputs are supported");
   int rc;
@@ -178,8 +179,8 @@ static int block_stats_impl(const void* q, const void* k, const void* v, float* 
   }
   return launch_status(pasa::launch_block_stats(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh,
                                                 (int)(seq_len - text_len), (int)seq_len, (int)head_dim,
-                                                (int)block_size, (int)group_size, rm, (float*)workspace, split,
-                                                (hipStream_t)stream),
+                                                (int)block_size, (int)group_size, rm, tm_copies,
+                                                (float*)workspace, split, (hipStream_t)stream),
                        "pasa_block_stats");
 }
 
@@ -200,7 +201,7 @@ int pasa_block_stats(const void* q, const void* k, const void* v, float* qc, flo
                      float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
                      int64_t head_dim, int64_t block_size, int64_t group_size, int dtype, void* stream) {
   return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
-                          group_size, dtype, nullptr, nullptr, 0, stream);
+                          group_size, dtype, nullptr, nullptr, nullptr, 0, stream);
 }
 
 int pasa_block_stats_ws(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
@@ -208,7 +209,7 @@ int pasa_block_stats_ws(const void* q, const void* k, const void* v, float* qc, 
                         int64_t head_dim, int64_t block_size, int64_t group_size, int dtype, void* workspace,
                         size_t workspace_bytes, void* stream) {
   return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
-                          group_size, dtype, nullptr, workspace, workspace_bytes, stream);
+                          group_size, dtype, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 // The placement's row map, after checking it fits the slices it will address.
@@ -230,16 +231,18 @@ static int check_placement(const pasa_placement_t* pl, int64_t bh, int64_t seq_l
   return PASA_OK;
 }
 
-int pasa_block_stats_placed(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
-                            float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
-                            int64_t head_dim, int64_t block_size, int64_t group_size,
-                            const pasa_placement_t* placement, int dtype, void* workspace,
+int pasa_block_stats_placed(const void* q, const void* k, const void* v, void* q_tm, void* k_tm, void* v_tm,
+                            float* qc, float* kc, float* vc, float* hnorm, float* hgroup, int64_t bh,
+                            int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
+                            int64_t group_size, const pasa_placement_t* placement, int dtype, void* workspace,
                             size_t workspace_bytes, void* stream) {
+  if (!q_tm || !k_tm || !v_tm) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats_placed: NULL pointer");
   pasa::RowMap rm;
   int rc;
   if ((rc = check_placement(placement, bh, seq_len, text_len, head_dim, block_size, &rm))) return rc;
+  void* const copies[3] = {q_tm, k_tm, v_tm};
   return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
-                          group_size, dtype, &rm, workspace, workspace_bytes, stream);
+                          group_size, dtype, &rm, copies, workspace, workspace_bytes, stream);
 }
 
 size_t pasa_select_workspace_bytes(int64_t bh, int64_t num_blocks) {

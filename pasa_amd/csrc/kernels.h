@@ -20,9 +20,11 @@ hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* 
 // rm: nullptr, or the token-major view of frame-major slices (D = 128, BT = 128).
 // split > 1: each group's blocks go to `split` workgroups, whose raw partial sums
 // (partials: [bh, NG, split, D, D] fp32) a second kernel reduces in order into hgroup.
+// rm: frame-major q, k, v (token-major view); tm_copies[3] then receive that view of q, k, v.
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
-                              int BT, int G, const RowMap* rm, float* partials, int split, hipStream_t stream);
+                              int BT, int G, const RowMap* rm, void* const* tm_copies, float* partials, int split,
+                              hipStream_t stream);
 int block_stats_split(int bh, int T, int D, int BT, int G);  // the split the launcher is given by the C ABI
 
 hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,

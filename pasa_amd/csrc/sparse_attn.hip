@@ -559,8 +559,8 @@ constexpr int kSchedDsRead = 0x100;
 
 // ALL: dense attention (every key block exact, no selection read, no correction); a
 // separate instantiation so that profiles tell the two launches apart.
-// PERM: q, k, v, o are frame-major and the attention runs on their token-major view
-// (rm); every row address goes through map_row.
+// PERM: q, k, v are the token-major view (as pasa_block_stats_placed writes it) and o
+// is stored frame-major: the store of a query row goes through map_row.
 // PAIR: two consecutive query blocks (or text query tiles) per workgroup (not ALL,
 // not PERM).  Video blocks visit NS selected tiles each, so their barriers match
 // (a shorter selection row, or a text pair spanning the prompt and the padding
@@ -645,7 +645,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const int64_t slice = (int64_t)bh * Ttot * D;
   const int qrow = qrow0 + qw * 32 + l32;
   const bool perm = PERM && slice_permuted(rm, bh);
-  const int qrow_st = perm ? map_row(qrow, rm) : qrow;  // stored row of this lane's query
+  const int qrow_st = perm ? map_row(qrow, rm) : qrow;  // frame-major row of this lane's output
 
   const uint32_t slice_bytes = (uint32_t)Ttot * D * 2u;
   const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
@@ -653,7 +653,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   bf16x8_t qf[D / 16];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks)
-    qf[ks] = as_bf16x8(buf_load16(qr, ((uint32_t)qrow_st * D + ks * 16 + h * 8) * 2u));
+    qf[ks] = as_bf16x8(buf_load16(qr, ((uint32_t)qrow * D + ks * 16 + h * 8) * 2u));
   // Complete the Q loads now: vector-memory waits the compiler would place at their
   // first use inside the loop would also wait for the tile loads in flight there.
   wait_vmcnt<0>();
@@ -697,27 +697,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const uint32_t kt_lds = ks_lds + tile_off;
   const uint32_t vt_lds = vs_lds + tile_off;
   // A tile is BT key rows starting at row `row0` of the slice (rows past the slice read as zero).
-  // Permuted slices: the lane's rows row0 + 16n + 4(qw + QWAVES vw) + lrow are fetched
-  // from their stored rows (computed for K, reused by the V load of the same tile).
-  int st_row[C::VW][BT / 16];
-  auto stored_rows = [&](int row0) {
-#pragma unroll
-    for (int vw = 0; vw < C::VW; ++vw)
-#pragma unroll
-      for (int n = 0; n < BT / 16; ++n)
-        st_row[vw][n] = map_row(row0 + 16 * n + 4 * (qw + C::QWAVES * vw) + lrow, rm);
-  };
   auto load_k = [&](int row0) {
-    if (perm) {
-      stored_rows(row0);
-#pragma unroll
-      for (int vw = 0; vw < C::VW; ++vw)
-#pragma unroll
-        for (int n = 0; n < BT / 16; ++n)
-          dma_load16_lds(kd, kt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256,
-                         (uint32_t)st_row[vw][n] * 256u + (k_lane[vw] & 255u), 0u);
-      return;
-    }
     const uint32_t soff = (uint32_t)row0 * 256u;
 #pragma unroll
     for (int vw = 0; vw < C::VW; ++vw)
@@ -725,16 +705,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int n = 0; n < BT / 16; ++n)
         dma_load16_lds(kd, kt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256, k_lane[vw] + 16 * n * 256, soff);
   };
-  auto load_v = [&](int row0) {  // permuted slices: row0 is the tile of the last load_k
-    if (perm) {
-#pragma unroll
-      for (int vw = 0; vw < C::VW; ++vw)
-#pragma unroll
-        for (int n = 0; n < BT / 16; ++n)
-          dma_load16_lds(vd, vt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256,
-                         (uint32_t)st_row[vw][n] * 256u + (v_lane0 & 255u), 0u);
-      return;
-    }
+  auto load_v = [&](int row0) {
     const uint32_t soff = (uint32_t)row0 * 256u;
 #pragma unroll
     for (int vw = 0; vw < C::VW; ++vw)

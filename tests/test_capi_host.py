@@ -296,8 +296,9 @@ def test_placed_entries_validation(lib):
     bs, sp = lib.pasa_block_stats_placed, lib.pasa_sparse_attn_packed_placed
     need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 40, 128, 128, 32)
 
-    def stats(pl, D=128, BT=128, T=1000, text=40, bh=2):
-        return bs(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, bh, T, text, D, BT, 32, pl, 0, None, 0, None)
+    def stats(pl, D=128, BT=128, T=1000, text=40, bh=2, copy=FAKE):
+        return bs(FAKE, FAKE, FAKE, FAKE, FAKE, copy, FAKE, FAKE, FAKE, FAKE, FAKE, bh, T, text, D, BT, 32, pl, 0,
+                  None, 0, None)
 
     def attn(pl, D=128, BT=128, T=1000, text=40, bh=2):
         return sp(FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, bh, T, text, text, D, BT, 32, 2, 1, pl, 0,
@@ -314,6 +315,7 @@ def test_placed_entries_validation(lib):
         big = Placement(2, (1 << 23) + 1, None, 1)                   # F*P > 2^24 rows
         assert fn(ctypes.byref(big), T=2 * ((1 << 23) + 1), text=0, bh=1) == -6
         assert lib.pasa_last_error()
+    assert stats(ctypes.byref(good), copy=None) == -1  # the token-major copies are outputs
 
 
 F16 = 1 << 40            # 16-byte aligned fake device addresses, far apart
