@@ -925,7 +925,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   };
   // A group's pack is two parts: kbar + V^T (part 2, into Vs) and Hbar^T (into Ks).
   // Part 2 of the next group loads while this group's Hbar^T product runs, and the
-  // next Hbar^T loads while the next group's scores and P.V^ run.
+  // next Hbar^T loads while the next group's scores and P.V^ run.  Two barriers per
+  // group: after P.V^ (part 2 of g read everywhere, Hbar^T of g landed) and after the
+  // Hbar^T product (Hbar^T of g read everywhere, part 2 of the next group landed).
   constexpr int HT_LOADS = PK::HT_BYTES / 1024 / C::WAVES;
   constexpr int P2_LOADS = PK::PART2 / 1024 / C::WAVES;
   auto load_part2 = [&](int g) {
@@ -948,12 +950,12 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   if (g >= 0) {  // phase 1 ended with a barrier after the last reads of Ks and Vs
     load_part2(g);
     load_ht(g);
+    wait_vmcnt<HT_LOADS>();    // this wave's part 2 of group g landed (Hbar^T may be in flight)
+    barrier_lds_reads_done();  // ... and every wave's
   }
   while (g >= 0) {
     const int gn = next_group(g);
     const uint32_t approx = approx_of(g);
-    wait_vmcnt<HT_LOADS>();    // this wave's part 2 of group g landed (Hbar^T may be in flight)
-    barrier_lds_reads_done();  // ... and every wave's
 
     f32x16_t sb;
 #pragma unroll
@@ -1023,13 +1025,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
             as_bf16x8(lds_ld<uint4>(Pvt, pv_base + et * 32 * PadTile<kGroup>::ROW_BYTES + s * 16));
         oacc[et] = mfma32(a, pbf[s], oacc[et]);
       }
-    barrier_lds_reads_done();  // every wave is done reading part 2 of group g
+    wait_vmcnt<0>();           // this wave's Hbar^T of group g landed (nothing else is in flight)
+    barrier_lds_reads_done();  // every wave is done reading part 2 of group g; Hbar^T of g is in place
     if (gn >= 0) load_part2(gn);
-    if (gn >= 0)
-      wait_vmcnt<P2_LOADS>();  // Hbar^T of group g landed (part 2 of gn may be in flight)
-    else
-      wait_vmcnt<0>();
-    barrier_lds_reads_done();
 
     const float f = psum * scale;
     f32x16_t racc[D / 32];
@@ -1048,7 +1046,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int et = 0; et < D / 32; ++et)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[et][r] = fmaf(racc[et][r], f, oacc[et][r]);
-    barrier_lds_reads_done();  // every wave is done reading Hbar^T
+    if (gn >= 0) wait_vmcnt<0>();  // this wave's part 2 of group gn landed
+    barrier_lds_reads_done();      // every wave is done reading Hbar^T of g; part 2 of gn is in place
     if (gn >= 0) load_ht(gn);
     g = gn;
   }
