@@ -211,6 +211,26 @@ def main() -> int:
     log(f"dense attention {kd_ms:.1f} ms ({dense_flops / kd_ms / 1e9:.0f} TFLOP/s); "
         f"PyTorch SDPA {sdpa_ms:.1f} ms ({dense_flops / sdpa_ms / 1e9:.0f} TFLOP/s)")
 
+    # What the vendor's bf16 GEMM (torch.matmul -> hipBLASLt) sustains on this GPU: the
+    # practical MFMA ceiling K4's roofline fraction is read against (the nominal peak
+    # assumes the 2.4 GHz maximum clock, which a full-chip MFMA load does not hold).
+    gn = 16384
+    ga = torch.randn(gn, gn, device=dev, dtype=torch.bfloat16)
+    gb = torch.randn(gn, gn, device=dev, dtype=torch.bfloat16)
+    gc = torch.empty(gn, gn, device=dev, dtype=torch.bfloat16)
+    for _ in range(2):
+        torch.matmul(ga, gb, out=gc)
+    ka.record()
+    for _ in range(5):
+        torch.matmul(ga, gb, out=gc)
+    kb.record()
+    torch.cuda.synchronize()
+    gemm_ms = ka.elapsed_time(kb) / 5
+    gemm_tflops = 2.0 * gn ** 3 / (gemm_ms * 1e-3) / 1e12
+    del ga, gb, gc
+    log(f"reference bf16 GEMM {gn}^3: {gemm_ms:.2f} ms, {gemm_tflops:.0f} TFLOP/s "
+        f"({gemm_tflops / PEAK_BF16_TFLOPS:.3f} of the nominal peak); K4 at {achieved / gemm_tflops:.3f} of it")
+
     # K6 row ops at the Wan-14B row shape (75,600 x 5120): the gated residual + norm2 call,
     # the heaviest of the block's four (reads x and h, writes h and the normalised row).
     from pasa_amd import modulate as MOD
@@ -330,6 +350,9 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
                      "traffic": traffic, "kernel": "k4_sparse_attn", "flops_per_launch": flops_k4},
         "cpu_baseline": cpu,
+        "reference_gemm": {"shape": f"{gn}x{gn}x{gn} bf16, torch.matmul (hipBLASLt)", "ms": round(gemm_ms, 3),
+                           "TFLOPs": round(gemm_tflops, 1), "frac_of_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+                           "k4_over_gemm": round(achieved / gemm_tflops, 4)},
         "stages_ms": {"k2_stats_and_pack": round(k2, 4), "k3_select": round(k3, 4),
                       "k4_sparse_attn": round(k4, 4), "k4_median": round(k4_med, 4)},
         "k1_permute": {"fwd_ms": round(k1f, 4), "fwd_GBps": round(k1f_gbps, 1),
