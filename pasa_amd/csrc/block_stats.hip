@@ -12,6 +12,8 @@
 // matrix), subtracts kc vc^T, reduces ||H_j||_F and adds H_j into the group
 // accumulator held in registers.  H_j is never written to memory; the group
 // mean is written once per group.  All statistics are fp32.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -233,9 +235,8 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   constexpr int TILE = BT * 256;
   __shared__ __attribute__((aligned(1024))) unsigned char Kb[2 * TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char Vb[2 * TILE];
-  __shared__ float red_sum[4][3 * D];
-  __shared__ float colstat[3 * D];
-  __shared__ float red_norm[4];
+  __shared__ float qpart[2][4][D];  // per-wave Q column sums of the last two blocks
+  __shared__ float npart[2][4];     // per-wave ||H_j||^2
 
   // Workgroup (g, part) of a split group takes the part-th of `split` equal runs of its blocks.
   const int g = blockIdx.x / split;
@@ -268,48 +269,40 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   const bool perm = PERM && slice_permuted(rm, bh);
   // Stored row of logical row r (rows past T are not permuted and read as zero).
   auto st = [&](int r) -> uint32_t { return (uint32_t)(perm ? map_row(r, rm) : r); };
-  auto load_kv = [&](int buf, int j) {
-    if (perm) {
-      uint32_t off[BT / 16];
-#pragma unroll
-      for (int n = 0; n < BT / 16; ++n) off[n] = st(j * BT + 16 * n + 4 * wave + lrow) * 256u + (t_lane & 255u);
-#pragma unroll
-      for (int n = 0; n < BT / 16; ++n)
-        dma_load16_lds(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off[n], 0u);
-#pragma unroll
-      for (int n = 0; n < BT / 16; ++n)
-        dma_load16_lds(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off[n], 0u);
-      return;
-    }
-    const uint32_t soff = (uint32_t)j * BT * 256u;
-#pragma unroll
-    for (int n = 0; n < BT / 16; ++n)
-      dma_load16_lds(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, t_lane + 16 * n * 256, soff);
-#pragma unroll
-    for (int n = 0; n < BT / 16; ++n)
-      dma_load16_lds(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, t_lane + 16 * n * 256, soff);
-  };
-  // Q: thread t holds rows 16p + t/16, 16-byte chunk t % 16, for p < 8.
+  // Load slot n of block j: K and V rows 16n + 4 wave + lane/16 (direct to LDS buffer
+  // buf) and Q rows 16n + t/16, chunk t % 16 (thread t, into registers).  A block's
+  // slots are issued spread over the previous block's work, so that no wave stalls
+  // issuing a block's worth of loads at once.
   const int prow = tid >> 4;
   const int pc = tid & 15;
-  auto load_q = [&](uint4 (&qv)[BT / 16], int j) {
-#pragma unroll
-    for (int p = 0; p < BT / 16; ++p)
-      qv[p] = buf_load16(qr, (st(j * BT + 16 * p + prow) * D + pc * 8) * 2u);
+  auto load_slot = [&](int buf, int j, int n, uint4& qdst) {
+    uint32_t off, soff;
+    if (perm) {
+      off = st(j * BT + 16 * n + 4 * wave + lrow) * 256u + (t_lane & 255u);
+      soff = 0u;
+    } else {
+      off = t_lane + 16 * n * 256;
+      soff = (uint32_t)j * BT * 256u;
+    }
+    dma_load16_lds(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
+    dma_load16_lds(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
+    qdst = buf_load16(qr, (st(j * BT + 16 * n + prow) * D + pc * 8) * 2u);
   };
 
   // Transposing operand reads: lane gets feature 32 ft + l32, tokens 4h + {0..3} (lo)
   // and 8 + 4h + {0..3} (hi) of token step s.
   const int g16 = lane >> 4;
   const int i16 = lane & 15;
-  int tofs[D / 32];
-#pragma unroll
-  for (int ft = 0; ft < D / 32; ++ft)
-    tofs[ft] = (4 * (g16 >> 1) + (i16 >> 2)) * 256 +
-               ((4 * (ft ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
-  auto frag = [&](const unsigned char* base, int ft, int s) {
-    const uint2 lo = lds_read_tr16(base, tofs[ft] + s * 16 * 256);
-    const uint2 hi = lds_read_tr16(base, tofs[ft] + s * 16 * 256 + 8 * 256);
+  auto tofs = [&](int ft) {
+    return (4 * (g16 >> 1) + (i16 >> 2)) * 256 +
+           ((4 * (ft ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
+  };
+  // This wave's feature tiles: K^T rows dq + 32 mt, V columns eq + 32 nt.
+  const int kofs[2] = {tofs(dq / 32), tofs(dq / 32 + 1)};
+  const int vofs[2] = {tofs(eq / 32), tofs(eq / 32 + 1)};
+  auto frag = [&](const unsigned char* base, int ofs, int s) {
+    const uint2 lo = lds_read_tr16(base, ofs + s * 16 * 256);
+    const uint2 hi = lds_read_tr16(base, ofs + s * 16 * 256 + 8 * 256);
     return __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
   };
 
@@ -320,127 +313,170 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) gacc[a][b][r] = 0.f;
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+
+  // The Q column sums and ||H_j||^2 of block j reach LDS as per-wave partials (buffer
+  // j & 1) and are finished after the next block's barrier, so a block costs one
+  // workgroup barrier.
+  auto finish = [&](int jj, int b, int nn) {
+    if (tid < D) {
+      const float sm = ((qpart[b][0][tid] + qpart[b][1][tid]) + qpart[b][2][tid]) + qpart[b][3][tid];
+      qc[((int64_t)bh * NT + jj) * D + tid] = sm / (float)nn;
+    } else if (tid == D) {
+      const float sn = ((npart[b][0] + npart[b][1]) + npart[b][2]) + npart[b][3];
+      hnorm[(int64_t)bh * NT + jj] = sqrtf(sn);
+    }
+  };
 
   uint4 qv[BT / 16], qn[BT / 16];
   if (j0 < j1) {
-    load_kv(0, j0);
-    load_q(qv, j0);
+#pragma unroll
+    for (int n = 0; n < BT / 16; ++n) load_slot(0, j0, n, qv[n]);
   }
-  for (int j = j0; j < j1; ++j) {
+  // One block.  PRE: block j+1 exists and its loads are issued here, slots 0 and 1 at
+  // once and slot s2 + 2 at MFMA step s2 (a compile-time choice, so that the MFMA loop
+  // is one basic block).
+  auto block = [&](auto pre_c, int j) {
+    constexpr bool PRE = decltype(pre_c)::value;
     const int buf = (j - j0) & 1;
     const int n = min(BT, T - j * BT);
     wait_vmcnt<0>();           // block j's K, V (LDS) and Q (registers) landed
     __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();  // every wave's parts; block j-1's readers of buffer buf^1 done
+    __builtin_amdgcn_s_barrier();  // every wave's parts; block j-1's tile reads and partials done
     asm volatile("" ::: "memory");
-    if (j + 1 < j1) {
-      load_kv(buf ^ 1, j + 1);
-      load_q(qn, j + 1);
+    if (j > j0) finish(j - 1, buf ^ 1, min(BT, T - (j - 1) * BT));
+    if (PRE) {
+      load_slot(buf ^ 1, j + 1, 0, qn[0]);
+      load_slot(buf ^ 1, j + 1, 1, qn[1]);
     }
     const unsigned char* Kt = Kb + buf * TILE;
     const unsigned char* Vt = Vb + buf * TILE;
-
-    // Column sums: Q from registers, K and V from the LDS tiles (same rows and chunk).
-    float ps[3][8];
+    if (PERM) {  // the token-major copies (rows past T hold text)
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ps[a][i] = 0.f;
-#pragma unroll
-    for (int p = 0; p < BT / 16; ++p) {
-      const int r = 16 * p + prow;
-      const int off = r * 256 + ((pc ^ (4 * (r & 3))) << 4);
-      const uint4 kx = lds_ld<uint4>(Kt, off);
-      const uint4 vx = lds_ld<uint4>(Vt, off);
-      if (PERM && j * BT + r < T) {  // the token-major copies (rows past T hold text)
-        const int64_t e = slice + (int64_t)(j * BT + r) * D + pc * 8;
-        *reinterpret_cast<uint4*>(qt + e) = qv[p];
-        *reinterpret_cast<uint4*>(kt + e) = kx;
-        *reinterpret_cast<uint4*>(vt + e) = vx;
+      for (int p = 0; p < BT / 16; ++p) {
+        const int r = 16 * p + prow;
+        if (j * BT + r < T) {
+          const int off = r * 256 + ((pc ^ (4 * (r & 3))) << 4);
+          const int64_t e = slice + (int64_t)(j * BT + r) * D + pc * 8;
+          *reinterpret_cast<uint4*>(qt + e) = qv[p];
+          *reinterpret_cast<uint4*>(kt + e) = lds_ld<uint4>(Kt, off);
+          *reinterpret_cast<uint4*>(vt + e) = lds_ld<uint4>(Vt, off);
+        }
       }
-      float f[8];
-      unpack8(qv[p], f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ps[0][i] += f[i];
-      unpack8(kx, f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ps[1][i] += f[i];
-      unpack8(vx, f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ps[2][i] += f[i];
     }
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float x = ps[a][i];
-        x += __shfl_xor(x, 16, 64);
-        x += __shfl_xor(x, 32, 64);
-        ps[a][i] = x;
-      }
-    if (lane < 16) {
-#pragma unroll
-      for (int a = 0; a < 3; ++a)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) red_sum[wave][a * D + lane * 8 + i] = ps[a][i];
-    }
-    __syncthreads();
-    const float nf = (float)n;
-    for (int idx = tid; idx < 3 * D; idx += 256) {
-      float sm = ((red_sum[0][idx] + red_sum[1][idx]) + red_sum[2][idx]) + red_sum[3][idx];
-      const int a = idx / D;
-      const int d = idx - a * D;
-      if (a < 2) sm = sm / nf;
-      colstat[idx] = sm;
-      float* dst = a == 0 ? qc : (a == 1 ? kc : vc);
-      dst[((int64_t)bh * NT + j) * D + d] = sm;
-    }
-    __syncthreads();
 
-    // H_j quadrant = K^T V (rows >= n are zero in both tiles).
-    f32x16_t acc[2][2];
+    // H_j quadrant = K^T V, and on the same fragments the K and V column sums: K^T 1
+    // (element r of a lane: feature dq + 32 mt + mfma32_row(r, h), the row layout the
+    // correction needs) and 1^T V (every element: feature eq + 32 nt + l32, the lane's
+    // column).  Rows >= n are zero in both tiles.  Before it, the Q column sums: thread
+    // (prow, pc) adds its rows 16 p + prow of chunk pc.
+    f32x16_t acc[2][2], ak[2], av[2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 2; ++a) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ak[a][r] = av[a][r] = 0.f;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+    }
+    float ps[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ps[i] = 0.f;
+#pragma unroll
+    for (int p = 0; p < BT / 16; ++p) {
+      float f[8];
+      unpack8(qv[p], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps[i] += f[i];
+    }
 #pragma unroll
     for (int s2 = 0; s2 < BT / 16; ++s2) {
+      if (PRE && s2 + 2 < BT / 16) load_slot(buf ^ 1, j + 1, s2 + 2, qn[s2 + 2]);
       bf16x8_t af[2], bfr[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) af[mt] = frag(Kt, dq / 32 + mt, s2);
+      for (int mt = 0; mt < 2; ++mt) af[mt] = frag(Kt, kofs[mt], s2);
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) bfr[nt] = frag(Vt, eq / 32 + nt, s2);
+      for (int nt = 0; nt < 2; ++nt) bfr[nt] = frag(Vt, vofs[nt], s2);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(af[mt], bfr[nt], acc[mt][nt]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) ak[mt] = mfma32(af[mt], ones, ak[mt]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) av[nt] = mfma32(ones, bfr[nt], av[nt]);
     }
-    float nrm = 0.f;
+    // The four 16-lane rows of the wave hold the same chunks: add them with the swaps.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float x = ps[i];
+      {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
+      ps[i] = halves_sum(x);
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qpart[buf][wave][lane * 8 + i] = ps[i];
+    }
+    // Means: sum / n, a product by the exact reciprocal when n is a power of two (every
+    // full block), else the correctly rounded division.
+    const float nf = (float)n;
+    f32x16_t (&km)[2] = ak;  // the sums become the means in place
+    if ((n & (n - 1)) == 0) {
+      const float rn = 1.f / nf;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) km[mt][r] = ak[mt][r] * rn;
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) km[mt][r] = ak[mt][r] / nf;
+    }
+    if (eq == 0 && l32 == 0) {  // waves 0 and 2, lanes 0 and 32: kc of features dq .. dq + 63
+      float* dst = kc + ((int64_t)bh * NT + j) * D + dq + 4 * h;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+          *reinterpret_cast<float4*>(dst + 32 * mt + 8 * rq) =
+              make_float4(km[mt][4 * rq], km[mt][4 * rq + 1], km[mt][4 * rq + 2], km[mt][4 * rq + 3]);
+    }
+    if (dq == 0 && h == 0) {  // waves 0 and 1: vc of features eq .. eq + 63
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) vc[((int64_t)bh * NT + j) * D + eq + 32 * nt + l32] = av[nt][0];
+    }
+    float nrm[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int e = eq + nt * 32 + l32;
-        const float vsum = colstat[2 * D + e];
+      for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int d = dq + mt * 32 + mfma32_row(r, h);
-          const float hv = acc[mt][nt][r] - colstat[D + d] * vsum;
-          nrm += hv * hv;
+          const float hv = acc[mt][nt][r] - km[mt][r] * av[nt][0];
+          nrm[r & 3] += hv * hv;
           gacc[mt][nt][r] += hv;
         }
-      }
-    nrm = wave_sum(nrm);
-    if (lane == 0) red_norm[wave] = nrm;
-    __syncthreads();
-    if (tid == 0) {
-      const float sn = ((red_norm[0] + red_norm[1]) + red_norm[2]) + red_norm[3];
-      hnorm[(int64_t)bh * NT + j] = sqrtf(sn);
-    }
+    const float nsum = wave_sum_xor((nrm[0] + nrm[1]) + (nrm[2] + nrm[3]));
+    if (lane == 0) npart[buf][wave] = nsum;
 #pragma unroll
     for (int p = 0; p < BT / 16; ++p) qv[p] = qn[p];
+  };
+  for (int j = j0; j < j1; ++j) {
+    if (j + 1 < j1)
+      block(std::true_type{}, j);
+    else
+      block(std::false_type{}, j);
+  }
+  if (j0 < j1) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // the last block's partials
+    asm volatile("" ::: "memory");
+    finish(j1 - 1, (j1 - 1 - j0) & 1, min(BT, T - (j1 - 1) * BT));
   }
 
   if (PERM && g == 0 && part == 0) {  // the text rows, in place in both layouts
