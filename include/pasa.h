@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 8
+#define PASA_ABI_VERSION 9
 
 typedef enum {
   PASA_OK = 0,
@@ -108,6 +108,8 @@ int pasa_permute(const void* src0, const void* src1, const void* src2,
  *   hnorm[j] = || sum_t (k_t - kc[j]) v_t^T ||_F                        (fp32 [BH,NT])
  *   hgroup[g] = (1/G) * sum_{j in group g, j < NT} H_j                 (fp32 [BH,NG,D,D])
  * with NG = ceil(NT / G).  H_j is never materialised in memory.
+ * dtype: PASA_DTYPE_BF16, or PASA_DTYPE_F16 at head_dim 128 (q, k, v; the statistics
+ * are fp32 either way).
  * Replaces: fused_chunk_reduce group_pisa_attention.py:268-288 (kernel :66-129,
  *   sqrt at :287) and compute_h_group :291-301. */
 int pasa_block_stats(const void* q, const void* k, const void* v,
@@ -172,7 +174,10 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
  * gamma_literal = 0 rescales it with A and L.
  * scale: the natural-log softmax scale s (> 0); scores use s*log2(e) in base 2
  * and the first-order term uses s.  Group size is 32 on this path.
- * workspace: >= pasa_sparse_attn_workspace_bytes(...) bytes (packed bf16 phase-2
+ * dtype: PASA_DTYPE_BF16, or PASA_DTYPE_F16 at head_dim 128 (q, k, v, o and the
+ * packed phase-2 operands; P is rounded to the same type before P.V, as the
+ * reference casts it to v's dtype).
+ * workspace: >= pasa_sparse_attn_workspace_bytes(...) bytes (packed phase-2
  * operands, written by this call).
  * Replaces: pisa_pg_fwd_kernel group_pisa_attention.py:135-262, launched at :380-396. */
 int pasa_sparse_attn(const void* q, const void* k, const void* v,
@@ -190,13 +195,15 @@ size_t pasa_sparse_attn_workspace_bytes(int64_t bh, int64_t seq_len, int64_t tex
 /* The two halves of pasa_sparse_attn, for callers that reuse the packed phase-2
  * operands or time the attention kernel alone.
  * pasa_pack_phase2 writes, per (slice, group of 32 key blocks), kbar, the value
- * sums (transposed) and Hbar (transposed) as bf16 into `pack`
+ * sums (transposed) and Hbar (transposed) in `dtype` (bf16, or fp16 at head_dim 128;
+ * it must be the dtype of the attention call that reads the pack) into `pack`
  * (pasa_sparse_attn_workspace_bytes(...) bytes).
- * Replaces: the bf16 stores of kc/vc (group_pisa_attention.py:118-119) and the
- * bf16 cast of h_group at its use (:251). */
+ * Replaces: the stores of kc/vc in the input dtype (group_pisa_attention.py:118-119)
+ * and the cast of h_group at its use (:251). */
 int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
                      size_t pack_bytes, int64_t bh, int64_t seq_len, int64_t text_len,
-                     int64_t head_dim, int64_t block_size, int64_t group_size, void* stream);
+                     int64_t head_dim, int64_t block_size, int64_t group_size, int dtype,
+                     void* stream);
 
 /* K4 proper on operands packed by pasa_pack_phase2 (same arguments and semantics
  * as pasa_sparse_attn otherwise).
@@ -245,7 +252,7 @@ typedef struct {
 
 /* The placement folded into K2 and K4.  pasa_block_stats_placed reads frame-major
  * q, k, v once: it computes the statistics of their token-major view and writes that
- * view to q_tm, k_tm, v_tm (device bf16 [BH, seq_len, head_dim], text rows copied in
+ * view to q_tm, k_tm, v_tm (device [BH, seq_len, head_dim] in q's dtype, text rows copied in
  * place) in the same pass.  pasa_sparse_attn_packed_placed takes those token-major
  * copies as q, k, v and stores o frame-major.  Together they equal pasa_permute ->
  * pasa_block_stats -> ... -> pasa_sparse_attn_packed -> inverse pasa_permute bit for
@@ -275,7 +282,7 @@ int pasa_sparse_attn_packed_placed(const void* q, const void* k, const void* v, 
  * (every key block exact; no statistics, selection or correction).  With a text
  * segment (text_len > 0) the attention is block-diagonal over [0, seq_len -
  * text_len + text_valid) and the padding rows after it, the cu_seqlens semantics
- * of the dense HunyuanVideo path.  bf16, head_dim 128; no workspace.
+ * of the dense HunyuanVideo path.  bf16 or fp16, head_dim 128; no workspace.
  * Replaces: the dense warm-up branch of the processors, flash_attention /
  * F.scaled_dot_product_attention (svg/models/wan/attention.py:299-301, :378-379;
  * svg/models/hyvideo/attention.py:450-476, :671-672). */

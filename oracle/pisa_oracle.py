@@ -23,7 +23,11 @@ How each part is pinned (tests/test_oracle_*.py):
                  == softmax attention, constant blocks == softmax attention,
                  key-shift invariance, value-shift equivariance (consistent
                  Gamma), G = 1 == brute-force first-order Taylor, O(eps^2)
-                 convergence of the first-order term.
+                 convergence of the first-order term;
+  rounding     - bf16_ulp / f16_ulp against the spacing of adjacent representable
+                 values, and the reference-precision emulation: outputs
+                 representable in the requested type, equal to the unrounded
+                 oracle to within that type's rounding.
 Every function above has at least one such check: none is "parity unpinned".
 """
 from __future__ import annotations
@@ -178,8 +182,15 @@ def selection_mask(idx: torch.Tensor, num_blocks: int) -> np.ndarray:
 # K4: attention, closed form (group_pisa_attention.py:154-262)
 # ----------------------------------------------------------------------------
 
-def _bf16(x: torch.Tensor) -> torch.Tensor:
-    return x.to(torch.bfloat16).to(x.dtype)
+def _rounding(ref_precision):
+    """The storage rounding ``ref_precision`` asks for: False -> none, True -> bf16, a
+    torch dtype (bfloat16 or float16) -> that type (the reference rounds to its input
+    dtype: `p.to(v.dtype)`, stats stored like q)."""
+    if ref_precision is False or ref_precision is None:
+        return lambda x: x
+    dt = torch.bfloat16 if ref_precision is True else ref_precision
+    assert dt in (torch.bfloat16, torch.float16), dt
+    return lambda x: x.to(dt).to(x.dtype)
 
 
 def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scale, gamma,
@@ -207,7 +218,7 @@ def _attention_one(q, k, v, kc, vc, hgroup, idx, n, block_size, group_size, scal
     # zero-order block index -> group, padded to NG*G
     npad = NG * group_size - NT
     nlen = n.to(dt)
-    rnd = _bf16 if ref_precision else (lambda x: x)
+    rnd = _rounding(ref_precision)
     kc, vc, hgroup = rnd(kc), rnd(vc), rnd(hgroup)
     for i0 in range(0, NT, chunk):
         i1 = min(NT, i0 + chunk)
@@ -270,8 +281,10 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
     indices: optional [B, H, NT, NS] selection to use instead of computing it
     (isolates the attention stage from score rounding).
     gamma: 'literal' (reference: Gamma never rescaled) or 'consistent'.
-    ref_precision: emulate the reference's bf16 roundings in the attention stage
-    (the selection stays fp32); see _attention_one.
+    ref_precision: emulate the reference's roundings in the attention stage (the
+    selection stays fp32); see _attention_one.  True rounds to bf16; a dtype
+    (torch.bfloat16 or torch.float16) rounds to that type, the reference's rounding
+    for inputs of that dtype.
     text_tokens: the last ``text_tokens`` rows form a text segment (HunyuanVideo puts
     its text tokens last, svg/models/hyvideo/attention.py:308-310; the reference
     documents the intent at group_pisa_attention.py:317, 330-333 but runs PISA over
@@ -322,9 +335,9 @@ def pisa_pg_attention(q, k, v, density: float = 0.15, block_size: int = 64, grou
             # ref_precision: P cast to bf16 before the P.V product, as the exact phase
             # does (:185) and as flash attention does on the reference's dense path; the
             # row sum stays fp32 (:184)
-            pv = _bf16(p) if ref_precision else p
-            o = torch.matmul(pv, full[2][b, k0:k1]) / p.sum(-1, keepdim=True)
-            out[b, r0:r1] = _bf16(o) if ref_precision else o
+            rnd = _rounding(ref_precision)
+            o = torch.matmul(rnd(p), full[2][b, k0:k1]) / p.sum(-1, keepdim=True)
+            out[b, r0:r1] = rnd(o)
     out = out.reshape(B, H, T, D)
     if return_aux:
         return out, dict(stats=st, hgroup=hgroup, scores=scores, idx=idx)
@@ -453,21 +466,33 @@ def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(ax)) - 7)
 
 
-def parity_metrics(out: torch.Tensor, ref: torch.Tensor) -> dict:
+def f16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of fp16 numbers at |x| (11 significant bits, subnormal spacing 2^-24 below
+    2^-14): 2^(max(floor(log2|x|), -14) - 10)."""
+    ax = x.abs().clamp_min(2.0 ** -14)
+    return torch.exp2(torch.floor(torch.log2(ax)) - 10)
+
+
+def ulp(x: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    """Spacing of ``dtype`` (bfloat16 or float16) numbers at |x|."""
+    return f16_ulp(x) if dtype == torch.float16 else bf16_ulp(x)
+
+
+def parity_metrics(out: torch.Tensor, ref: torch.Tensor, dtype=torch.bfloat16) -> dict:
     """Agreement of ``out`` with the fp32 reference ``ref``.
 
     cos, max_abs and max_abs_over_rms are the north_star figures.  ``excess_over_rms``
-    is max(|err| - ulp_bf16(|ref|)) / RMS(ref): the error left after allowing one
-    bf16 ulp of each reference element, the quantum of any bf16 result (the
-    reference stores P and its output in bf16).  ``bound_ok`` is cos >= 0.999 and
-    excess_over_rms <= 2e-2."""
+    is max(|err| - ulp(|ref|)) / RMS(ref): the error left after allowing one ulp of
+    the output type ``dtype`` (bf16 or fp16) at each reference element, the quantum of
+    any result stored in it (the reference stores P and its output in the input
+    dtype).  ``bound_ok`` is cos >= 0.999 and excess_over_rms <= 2e-2."""
     a = out.detach().to(torch.float64).reshape(-1).cpu()
     b = ref.detach().to(torch.float64).reshape(-1).cpu()
     cos = float(torch.dot(a, b) / (a.norm() * b.norm()).clamp_min(1e-300))
     e = (a - b).abs()
     err = float(e.max())
     rms = float(b.pow(2).mean().sqrt())
-    excess = float((e - bf16_ulp(b)).clamp_min(0).max())
+    excess = float((e - ulp(b, dtype)).clamp_min(0).max())
     return dict(cos=cos, max_abs=err, rms=rms, max_abs_over_rms=err / max(rms, 1e-300),
                 excess_over_rms=excess / max(rms, 1e-300),
                 bound_ok=bool(cos >= 0.999 and excess <= 2e-2 * rms))

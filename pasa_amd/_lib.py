@@ -70,7 +70,7 @@ SIGNATURES = {
     "pasa_sparse_attn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "pasa_sparse_attn_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                         _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
-    "pasa_pack_phase2": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "pasa_pack_phase2": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "pasa_sparse_attn_packed": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _dbl, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
     "pasa_block_stats_placed": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
@@ -84,7 +84,7 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i64, _dbl, _vp]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Size of the static device array behind pasa_sparse_attn_noalloc (PASA_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 64 << 20

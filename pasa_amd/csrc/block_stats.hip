@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 // from the registers (Q) and LDS tiles (K, V) the column sums read it from, and the
 // workgroup of group 0 copies the text rows [T, Tslice), which stay in place.
 // BT 128 (two 64 KB buffer pairs: one workgroup per CU) or 64 (two per CU).
-template <int BT, bool PERM>
+template <int BT, bool PERM, typename E = Bf16>
 __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, float* __restrict__ qc, float* __restrict__ kc,
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   auto frag = [&](const unsigned char* base, int ofs, int s) {
     const uint2 lo = lds_read_tr16(base, ofs + s * 16 * 256);
     const uint2 hi = lds_read_tr16(base, ofs + s * 16 * 256 + 8 * 256);
-    return __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
+    return as_vec8<E>((u32x4_t){lo.x, lo.y, hi.x, hi.y});
   };
 
   f32x16_t gacc[2][2];
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) gacc[a][b][r] = 0.f;
-  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  const typename E::vec8 ones = as_vec8<E>((u32x4_t){E::kOne2, E::kOne2, E::kOne2, E::kOne2});
 
   // The Q column sums and ||H_j||^2 of block j reach LDS as per-wave partials (buffer
   // j & 1) and are finished after the next block's barrier, so a block costs one
@@ -386,14 +386,14 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
 #pragma unroll
     for (int p = 0; p < BT / 16; ++p) {
       float f[8];
-      unpack8(qv[p], f);
+      E::widen8(qv[p], f);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ps[i] += f[i];
     }
 #pragma unroll
     for (int s2 = 0; s2 < BT / 16; ++s2) {
       if (PRE && s2 + 2 < BT / 16) load_slot(buf ^ 1, j + 1, s2 + 2, qn[s2 + 2]);
-      bf16x8_t af[2], bfr[2];
+      typename E::vec8 af[2], bfr[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) af[mt] = frag(Kt, kofs[mt], s2);
 #pragma unroll
@@ -401,11 +401,11 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(af[mt], bfr[nt], acc[mt][nt]);
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = E::mfma(af[mt], bfr[nt], acc[mt][nt]);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) ak[mt] = mfma32(af[mt], ones, ak[mt]);
+      for (int mt = 0; mt < 2; ++mt) ak[mt] = E::mfma(af[mt], ones, ak[mt]);
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) av[nt] = mfma32(ones, bfr[nt], av[nt]);
+      for (int nt = 0; nt < 2; ++nt) av[nt] = E::mfma(ones, bfr[nt], av[nt]);
     }
     // The four 16-lane rows of the wave hold the same chunks: add them with the swaps.
 #pragma unroll
@@ -546,27 +546,38 @@ int block_stats_split(int bh, int T, int D, int BT, int G) {
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
                               int BT, int G, const RowMap* rm, void* const* tm_copies, float* partials, int split,
-                              hipStream_t stream) {
+                              bool f16, hipStream_t stream) {
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + G - 1) / G;
   if (split < 1 || split > G || (split > 1 && (partials == nullptr || D != 128 || (BT != 128 && BT != 64))))
     return hipErrorInvalidValue;
+  if (f16 && D != 128) return hipErrorInvalidValue;  // fp16 inputs: the D = 128 kernels only
   dim3 grid(NG * split, bh);
   auto a = (const uint16_t*)q;
   auto b = (const uint16_t*)k;
   auto c = (const uint16_t*)v;
+  auto dma = [&](auto kern, const RowMap& map, void* const* cp) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm, hgroup, T, Tslice, NT, G, map,
+                       split, partials, cp ? (uint16_t*)cp[0] : nullptr, cp ? (uint16_t*)cp[1] : nullptr,
+                       cp ? (uint16_t*)cp[2] : nullptr);
+  };
   if (rm != nullptr) {  // token-major view of frame-major slices: D = 128, BT = 128 only
     if (D != 128 || BT != 128 || tm_copies == nullptr) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k2_block_stats_dma<128, true>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, *rm, split, partials, (uint16_t*)tm_copies[0],
-                       (uint16_t*)tm_copies[1], (uint16_t*)tm_copies[2]);
-  } else if (D == 128 && BT == 128)
-    hipLaunchKernelGGL((k2_block_stats_dma<128, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials, nullptr, nullptr, nullptr);
-  else if (D == 128 && BT == 64)
-    hipLaunchKernelGGL((k2_block_stats_dma<64, false>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc, hnorm,
-                       hgroup, T, Tslice, NT, G, RowMap{}, split, partials, nullptr, nullptr, nullptr);
-  else if (D == 64 && BT == 128)
+    if (f16)
+      dma(k2_block_stats_dma<128, true, F16>, *rm, tm_copies);
+    else
+      dma(k2_block_stats_dma<128, true, Bf16>, *rm, tm_copies);
+  } else if (D == 128 && BT == 128) {
+    if (f16)
+      dma(k2_block_stats_dma<128, false, F16>, RowMap{}, nullptr);
+    else
+      dma(k2_block_stats_dma<128, false, Bf16>, RowMap{}, nullptr);
+  } else if (D == 128 && BT == 64) {
+    if (f16)
+      dma(k2_block_stats_dma<64, false, F16>, RowMap{}, nullptr);
+    else
+      dma(k2_block_stats_dma<64, false, Bf16>, RowMap{}, nullptr);
+  } else if (D == 64 && BT == 128)
     hipLaunchKernelGGL((k2_block_stats<64, 128>), grid, dim3(256), 0, stream, a, b, c, qc, kc, vc,
                        hnorm, hgroup, T, Tslice, NT, G);
   else if (D == 64 && BT == 64)

@@ -153,15 +153,26 @@ int pasa_permute(const void* src0, const void* src1, const void* src2, void* dst
                        "pasa_permute");
 }
 
+// The attention path's 16-bit tensors: bf16, or fp16 at head_dim 128 (the D = 64 kernels
+// are bf16 only).
+static int check_attn_dtype(int dtype, int64_t head_dim, const char* what) {
+  if (dtype == PASA_DTYPE_BF16) return PASA_OK;
+  if (dtype == PASA_DTYPE_F16) {
+    if (head_dim == 128) return PASA_OK;
+    return fail(PASA_ERR_DTYPE, "%s: fp16 inputs need head_dim 128 (got %lld)", what, (long long)head_dim);
+  }
+  return fail(PASA_ERR_DTYPE, "%s: dtype %d is not bf16 or fp16", what, dtype);
+}
+
 static int block_stats_impl(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
                             float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t head_dim, int64_t block_size, int64_t group_size, int dtype,
                             const pasa::RowMap* rm, void* const* tm_copies, void* workspace,
                             size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
-  if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_block_stats: only bf16 inputs are supported");
   int rc;
   if ((rc = check_head_dim(head_dim))) return rc;
+  if ((rc = check_attn_dtype(dtype, head_dim, "pasa_block_stats"))) return rc;
   if ((rc = check_block(block_size))) return rc;
   if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
   if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
@@ -180,7 +191,8 @@ static int block_stats_impl(const void* q, const void* k, const void* v, float* 
   return launch_status(pasa::launch_block_stats(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh,
                                                 (int)(seq_len - text_len), (int)seq_len, (int)head_dim,
                                                 (int)block_size, (int)group_size, rm, tm_copies,
-                                                (float*)workspace, split, (hipStream_t)stream),
+                                                (float*)workspace, split, dtype == PASA_DTYPE_F16,
+                                                (hipStream_t)stream),
                        "pasa_block_stats");
 }
 
@@ -331,13 +343,15 @@ static int check_pack(const void* pack, size_t pack_bytes, int64_t bh, int64_t s
 
 int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack, size_t pack_bytes,
                      int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
-                     int64_t group_size, void* stream) {
+                     int64_t group_size, int dtype, void* stream) {
   if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_pack_phase2: NULL pointer");
   int rc;
   if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
+  if ((rc = check_attn_dtype(dtype, head_dim, "pasa_pack_phase2"))) return rc;
   if ((rc = check_pack(pack, pack_bytes, bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
   return launch_status(pasa::launch_pack_phase2(kc, vc, hgroup, pack, (int)bh, (int)(seq_len - text_len),
-                                                (int)head_dim, (int)block_size, (hipStream_t)stream),
+                                                (int)head_dim, (int)block_size, dtype == PASA_DTYPE_F16,
+                                                (hipStream_t)stream),
                        "pasa_pack_phase2");
 }
 
@@ -348,9 +362,9 @@ static int check_attn_args(const void* q, const void* k, const void* v, const in
                            int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype) {
   (void)idx;
   if (!q || !k || !v || !selmask || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
-  if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_sparse_attn: only bf16 inputs are supported");
   int rc;
   if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
+  if ((rc = check_attn_dtype(dtype, head_dim, "pasa_sparse_attn"))) return rc;
   if (text_valid < 0 || text_valid > text_len)
     return fail(PASA_ERR_TEXT_SEGMENT, "text_valid=%lld must be in [0, text_len=%lld]", (long long)text_valid,
                 (long long)text_len);
@@ -375,7 +389,7 @@ static int sparse_attn_packed_impl(const void* q, const void* k, const void* v, 
   return launch_status(pasa::launch_sparse_attn(q, k, v, pack, idx, selmask, o, (float)scale, (int)bh,
                                                 (int)(seq_len - text_len), (int)text_len, (int)text_valid,
                                                 (int)head_dim, (int)block_size, (int)ns, gamma_literal, rm,
-                                                (hipStream_t)stream),
+                                                dtype == PASA_DTYPE_F16, (hipStream_t)stream),
                        "pasa_sparse_attn");
 }
 
@@ -414,7 +428,7 @@ int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* k
   if ((rc = check_pack(workspace, workspace_bytes, bh, seq_len, text_len, head_dim, block_size, group_size)))
     return rc;
   if ((rc = pasa_pack_phase2(kc, vc, hgroup, workspace, workspace_bytes, bh, seq_len, text_len, head_dim,
-                             block_size, group_size, stream)))
+                             block_size, group_size, dtype, stream)))
     return rc;
   return pasa_sparse_attn_packed(q, k, v, workspace, workspace_bytes, idx, selmask, o, scale, bh, seq_len,
                                  text_len, text_valid, head_dim, block_size, group_size, ns, gamma_literal,
@@ -493,7 +507,7 @@ int pasa_sparse_attn_noalloc(const void* q, const void* k, const void* v, const 
   void* pack = nullptr;
   if ((rc = scratch_address(stream, &pack))) return rc;
   if ((rc = pasa_pack_phase2(kc, vc, hgroup, pack, kScratchBytes, bh, seq_len, text_len, head_dim, block_size,
-                             group_size, stream)))
+                             group_size, dtype, stream)))
     return rc;
   return pasa_sparse_attn_packed(q, k, v, pack, kScratchBytes, idx, selmask, o, scale, bh, seq_len, text_len,
                                  text_valid, head_dim, block_size, group_size, ns, gamma_literal, dtype, stream);
@@ -503,9 +517,9 @@ int pasa_dense_attn(const void* q, const void* k, const void* v, void* o, double
                     int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim, int dtype,
                     void* stream) {
   if (!q || !k || !v || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_dense_attn: NULL pointer");
-  if (dtype != PASA_DTYPE_BF16) return fail(PASA_ERR_DTYPE, "pasa_dense_attn: only bf16 inputs are supported");
   if (head_dim != 128) return fail(PASA_ERR_HEAD_DIM, "pasa_dense_attn: head_dim %lld != 128", (long long)head_dim);
   int rc;
+  if ((rc = check_attn_dtype(dtype, head_dim, "pasa_dense_attn"))) return rc;
   if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
   if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;
   if ((rc = check_text(seq_len, text_len, head_dim))) return rc;
@@ -516,7 +530,8 @@ int pasa_dense_attn(const void* q, const void* k, const void* v, void* o, double
   const int64_t grid = 8 * bh * cdiv(cdiv(seq_len - text_len, 128), 8) + 8 * cdiv(bh * (cdiv(text_len, 128) + 1), 8);
   if (grid > kMaxI32) return fail(PASA_ERR_OVERFLOW, "grid too large");
   return launch_status(pasa::launch_dense_attn(q, k, v, o, (float)scale, (int)bh, (int)(seq_len - text_len),
-                                               (int)text_len, (int)text_valid, (hipStream_t)stream),
+                                               (int)text_len, (int)text_valid, dtype == PASA_DTYPE_F16,
+                                               (hipStream_t)stream),
                        "pasa_dense_attn");
 }
 

@@ -181,6 +181,55 @@ __device__ __forceinline__ f32x16_t mfma32(const bf16x8_t& a, const bf16x8_t& b,
 // Row of the 32x32 D tile held by element r of a lane in half h (= lane / 32).
 __device__ __forceinline__ int mfma32_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
+// ---- 16-bit element types of the attention path --------------------------------
+// The D = 128 kernels take their q, k, v (and write o and the phase-2 pack) in bf16 or
+// fp16; everything else (statistics, scores, accumulation) is fp32.  Each type gives
+// its 8-element MFMA operand, the 32x32x16 MFMA, round-to-nearest-even packing of two
+// floats, and the widening of 8 packed values.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+struct Bf16 {
+  using vec8 = bf16x8_t;
+  static constexpr uint32_t kOne2 = 0x3F803F80u;  // two 1.0s
+  __device__ static __forceinline__ f32x16_t mfma(const vec8& a, const vec8& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  __device__ static __forceinline__ uint32_t bits(float x) { return f32_to_bf16_bits(x); }
+  __device__ static __forceinline__ void widen8(const uint4& c, float* out) { unpack8(c, out); }
+};
+
+struct F16 {
+  using vec8 = f16x8_t;
+  static constexpr uint32_t kOne2 = 0x3C003C00u;
+  __device__ static __forceinline__ f32x16_t mfma(const vec8& a, const vec8& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2_t));
+  }
+  __device__ static __forceinline__ uint32_t bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  __device__ static __forceinline__ void widen8(const uint4& c, float* out) {
+    const f16x8_t h = __builtin_bit_cast(f16x8_t, c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = (float)h[i];
+  }
+};
+
+template <typename E>
+__device__ __forceinline__ typename E::vec8 as_vec8(const uint4& c) {
+  return __builtin_bit_cast(typename E::vec8, c);
+}
+template <typename E>
+__device__ __forceinline__ typename E::vec8 as_vec8(const u32x4_t& c) {
+  return __builtin_bit_cast(typename E::vec8, c);
+}
+
 // ---- wave helpers -----------------------------------------------------------
 
 __device__ __forceinline__ float xor32(float x) {

@@ -24,7 +24,7 @@ hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* 
 hipError_t launch_block_stats(const void* q, const void* k, const void* v, float* qc, float* kc,
                               float* vc, float* hnorm, float* hgroup, int bh, int T, int Tslice, int D,
                               int BT, int G, const RowMap* rm, void* const* tm_copies, float* partials, int split,
-                              hipStream_t stream);
+                              bool f16, hipStream_t stream);
 int block_stats_split(int bh, int T, int D, int BT, int G);  // the split the launcher is given by the C ABI
 
 hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, const float* noise,
@@ -36,8 +36,9 @@ hipError_t launch_topk(const float* scores, int bh, int NT, int NS, int32_t* idx
 
 size_t k4_pack_bytes(int D, int BT);  // per (slice, group) phase-2 pack image
 
+// f16: the pack (and, below, q, k, v, o) hold fp16 instead of bf16 (D = 128 only).
 hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
-                              int bh, int T, int D, int BT, hipStream_t stream);
+                              int bh, int T, int D, int BT, bool f16, hipStream_t stream);
 
 // T: rows of the blocked (video) segment; text: rows of the text segment that
 // follows it in each slice (slices are T + text rows apart), the first text_valid of
@@ -45,14 +46,14 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
                               int bh, int T, int text, int text_valid, int D, int BT, int NS,
-                              int gamma_literal, const RowMap* rm, hipStream_t stream);
+                              int gamma_literal, const RowMap* rm, bool f16, hipStream_t stream);
 
 // Dense softmax attention with K4's phase-1 machinery (every key block exact, no
 // selection, no correction), D = 128.  T video rows, then `text` rows of which the
 // first text_valid are the prompt: rows attend within [0, T + text_valid) or within
 // the padding [T + text_valid, T + text).
 hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* o, float scale, int bh,
-                             int T, int text, int text_valid, hipStream_t stream);
+                             int T, int text, int text_valid, bool f16, hipStream_t stream);
 
 // ---- K5: processor prologue (RMSNorm + rotary embedding + head-major layout) ----
 constexpr int kNormHead = 1;       // RMSNorm over each head's D channels, weight [D]

@@ -141,7 +141,7 @@ __host__ __device__ __forceinline__ constexpr int xor_tile_byte(int row, int col
 // a 16-byte chunk: Hbar^T goes through LDS (coalesced fp32 reads of Hbar rows, column
 // reads from a padded tile), kbar rows are read as 32-byte runs, V^T columns with the
 // token index fastest across lanes.  Rounding is round-to-nearest-even, as everywhere.
-template <int BT>
+template <int BT, typename E = Bf16>
 __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
                                                    const float* __restrict__ vc,
                                                    const float* __restrict__ hgroup,
@@ -186,8 +186,7 @@ __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[i] = 0.f;
     }
-    const uint4 w = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                               pack_bf16x2(f[6], f[7]));
+    const uint4 w = make_uint4(E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7]));
     *(uint4*)(part2 + P::KB_OFF + xor_tile_byte(m, cc * 8)) = w;
   }
   // V^T: feature rows e x 4 chunks of 8 (permuted) tokens of the padded tile.
@@ -203,8 +202,7 @@ __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
       const int jj = g * kGroup + m;
       f[i] = jj < NT ? vb[(int64_t)jj * D + e] : 0.f;
     }
-    const uint4 w = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                               pack_bf16x2(f[6], f[7]));
+    const uint4 w = make_uint4(E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7]));
     *(uint4*)(part2 + P::VT_OFF + PadTile<kGroup>::chunk_byte(e, cc)) = w;
   }
   __syncthreads();
@@ -217,8 +215,7 @@ __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
     float f[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = hs[(cc * 8 + i) * HS + e];
-    const uint4 w = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                               pack_bf16x2(f[6], f[7]));
+    const uint4 w = make_uint4(E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7]));
     *(uint4*)(out + xor_tile_byte(e, cc * 8)) = w;
   }
 }
@@ -569,7 +566,7 @@ constexpr int kSchedDsRead = 0x100;
 // either block approximates; a group the other block approximates and this one
 // does not adds exact zeros here (p = 0, alpha = 1), so each block's result is the
 // one the unpaired kernel computes.
-template <int BT, bool ALL, bool PERM, bool PAIR = false>
+template <int BT, bool ALL, bool PERM, bool PAIR = false, typename E = Bf16>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(2, 2)))
 void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                         const uint16_t* __restrict__ v, const unsigned char* __restrict__ pack,
@@ -650,10 +647,10 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const uint32_t slice_bytes = (uint32_t)Ttot * D * 2u;
   const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
 
-  bf16x8_t qf[D / 16];
+  typename E::vec8 qf[D / 16];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks)
-    qf[ks] = as_bf16x8(buf_load16(qr, ((uint32_t)qrow * D + ks * 16 + h * 8) * 2u));
+    qf[ks] = as_vec8<E>(buf_load16(qr, ((uint32_t)qrow * D + ks * 16 + h * 8) * 2u));
   // Complete the Q loads now: vector-memory waits the compiler would place at their
   // first use inside the loop would also wait for the tile loads in flight there.
   wait_vmcnt<0>();
@@ -796,8 +793,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int ks = 0; ks < D / 16; ++ks)
 #pragma unroll
       for (int mt = 0; mt < BT / 32; ++mt) {
-        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks + tile_off, kofs[ks] + mt * 32 * 256));
-        sacc[mt] = mfma32(a, qf[ks], sacc[mt]);
+        const typename E::vec8 a = as_vec8<E>(lds_ld<uint4>(Ks + tile_off, kofs[ks] + mt * 32 * 256));
+        sacc[mt] = E::mfma(a, qf[ks], sacc[mt]);
       }
     // Keep 8 fragment reads in flight: each MFMA consumes a read issued 8 MFMAs
     // (~256 cycles) earlier, which covers the LDS latency.
@@ -846,7 +843,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     }
     // The row sum adds the fp32 p (as gpa.py:182-184 sums `score` before its bf16
     // cast) in four partial sums, then adds the tile's sum to the rescaled l.
-    bf16x8_t pf[BT / 16];
+    typename E::vec8 pf[BT / 16];
     float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < BT / 16; ++s) {
@@ -855,10 +852,10 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int i = 0; i < 4; ++i) {
         const float p0 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i], c, -m_run));
         const float p1 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i + 1], c, -m_run));
-        w[i] = pack_bf16x2(p0, p1);
+        w[i] = E::pack2(p0, p1);
         lsum[i] += p0 + p1;
       }
-      pf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+      pf[s] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
     }
     l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     // V_blk is waited for only now, so its load overlaps S and the softmax; the
@@ -874,8 +871,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int et = 0; et < D / 32; ++et) {
         const uint2 lo = lds_read_tr16(Vs + tile_off, vofs[et] + s * 16 * 256);
         const uint2 hi = lds_read_tr16(Vs + tile_off, vofs[et] + s * 16 * 256 + 8 * 256);
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, (u32x4_t){lo.x, lo.y, hi.x, hi.y});
-        oacc[et] = mfma32(a, pf[s], oacc[et]);
+        const typename E::vec8 a = as_vec8<E>((u32x4_t){lo.x, lo.y, hi.x, hi.y});
+        oacc[et] = E::mfma(a, pf[s], oacc[et]);
       }
     // Same read-ahead for the transposing V reads (two per MFMA): 4 MFMAs of operands in flight.
     {
@@ -962,8 +959,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int r = 0; r < 16; ++r) sb[r] = 0.f;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Vs, PK::KB_OFF + kofs[ks]));
-      sb = mfma32(a, qf[ks], sb);
+      const typename E::vec8 a = as_vec8<E>(lds_ld<uint4>(Vs, PK::KB_OFF + kofs[ks]));
+      sb = E::mfma(a, qf[ks], sb);
     }
     // Blocks of the group that are selected (or past NT) drop out: element r of a lane
     // in half h holds block mfma32_row(r, h) = 8(r >> 2) + 4h + (r & 3), so its keep
@@ -988,7 +985,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
     }
     float psum = 0.f;
-    bf16x8_t pbf[2];
+    typename E::vec8 pbf[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       uint32_t w[4];
@@ -998,9 +995,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         const float p0 = fast_exp2(fmaf(sb[r0], c, -m_new));
         const float p1 = fast_exp2(fmaf(sb[r0 + 1], c, -m_new));
         psum += p0 + p1;
-        w[i] = pack_bf16x2(p0, p1);
+        w[i] = E::pack2(p0, p1);
       }
-      pbf[s] = __builtin_bit_cast(bf16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+      pbf[s] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
     }
     // Gamma += sum_j p_j * n_j.  Every block holds BT rows except the last one, NT - 1,
     // which holds last_len: BT * sum(p) (exact, BT being a power of two), corrected for
@@ -1021,9 +1018,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int et = 0; et < D / 32; ++et) {
-        const bf16x8_t a =
-            as_bf16x8(lds_ld<uint4>(Pvt, pv_base + et * 32 * PadTile<kGroup>::ROW_BYTES + s * 16));
-        oacc[et] = mfma32(a, pbf[s], oacc[et]);
+        const typename E::vec8 a =
+            as_vec8<E>(lds_ld<uint4>(Pvt, pv_base + et * 32 * PadTile<kGroup>::ROW_BYTES + s * 16));
+        oacc[et] = E::mfma(a, pbf[s], oacc[et]);
       }
     wait_vmcnt<0>();           // this wave's Hbar^T of group g landed (nothing else is in flight)
     barrier_lds_reads_done();  // every wave is done reading part 2 of group g; Hbar^T of g is in place
@@ -1039,8 +1036,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int ks = 0; ks < D / 16; ++ks)
 #pragma unroll
       for (int et = 0; et < D / 32; ++et) {
-        const bf16x8_t a = as_bf16x8(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
-        racc[et] = mfma32(a, qf[ks], racc[et]);
+        const typename E::vec8 a = as_vec8<E>(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
+        racc[et] = E::mfma(a, qf[ks], racc[et]);
       }
 #pragma unroll
     for (int et = 0; et < D / 32; ++et)
@@ -1062,8 +1059,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       for (int rq = 0; rq < 4; ++rq) {
         const int e0 = et * 32 + 8 * rq + 4 * h;
         uint2 w;
-        w.x = pack_bf16x2(oacc[et][4 * rq + 0] * inv, oacc[et][4 * rq + 1] * inv);
-        w.y = pack_bf16x2(oacc[et][4 * rq + 2] * inv, oacc[et][4 * rq + 3] * inv);
+        w.x = E::pack2(oacc[et][4 * rq + 0] * inv, oacc[et][4 * rq + 1] * inv);
+        w.y = E::pack2(oacc[et][4 * rq + 2] * inv, oacc[et][4 * rq + 3] * inv);
         *(uint2*)(orow + e0) = w;
       }
   }
@@ -1078,16 +1075,23 @@ size_t k4_pack_bytes(int D, int BT) {
 }
 
 hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgroup, void* pack,
-                              int bh, int T, int D, int BT, hipStream_t stream) {
+                              int bh, int T, int D, int BT, bool f16, hipStream_t stream) {
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + kGroup - 1) / kGroup;
   dim3 grid(NG, bh);
   auto out = (unsigned char*)pack;
-  if (D == 128 && BT == 128)
-    hipLaunchKernelGGL((k4_pack_xor<128>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
-  else if (D == 128 && BT == 64)
-    hipLaunchKernelGGL((k4_pack_xor<64>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
-  else if (D == 64 && BT == 128)
+  if (f16 && D != 128) return hipErrorInvalidValue;
+  if (D == 128 && BT == 128) {
+    if (f16)
+      hipLaunchKernelGGL((k4_pack_xor<128, F16>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+    else
+      hipLaunchKernelGGL((k4_pack_xor<128, Bf16>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+  } else if (D == 128 && BT == 64) {
+    if (f16)
+      hipLaunchKernelGGL((k4_pack_xor<64, F16>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+    else
+      hipLaunchKernelGGL((k4_pack_xor<64, Bf16>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
+  } else if (D == 64 && BT == 128)
     hipLaunchKernelGGL((k4_pack<64, 128>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
   else if (D == 64 && BT == 64)
     hipLaunchKernelGGL((k4_pack<64, 64>), grid, dim3(256), 0, stream, kc, vc, hgroup, out, NT, NG);
@@ -1099,8 +1103,9 @@ hipError_t launch_pack_phase2(const float* kc, const float* vc, const float* hgr
 hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const void* pack,
                               const int32_t* idx, const uint32_t* selmask, void* o, float scale,
                               int bh, int T, int text, int text_valid, int D, int BT, int NS,
-                              int gamma_literal, const RowMap* rm, hipStream_t stream) {
+                              int gamma_literal, const RowMap* rm, bool f16, hipStream_t stream) {
   if (text > 0 && D != 128) return hipErrorInvalidValue;  // the text segment is a D = 128 feature
+  if (f16 && D != 128) return hipErrorInvalidValue;       // so are fp16 inputs
   if (text_valid < 0 || text_valid > text) return hipErrorInvalidValue;
   const int NT = (T + BT - 1) / BT;
   const int NG = (NT + kGroup - 1) / kGroup;
@@ -1116,26 +1121,36 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
   auto cc = (const uint16_t*)v;
   auto pk = (const unsigned char*)pack;
   auto oo = (uint16_t*)o;
+  // The D = 128 kernels, for either element type.
+  auto dma = [&](auto kern, dim3 g, int chunk, int n_text, const RowMap& map) {
+    hipLaunchKernelGGL(kern, g, dim3(256), 0, stream, a, b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, chunk,
+                       gamma_literal, text, text_valid, n_text, bh, map);
+  };
+  static_assert(K4D<128>::THREADS == 256 && K4D<64, true>::THREADS == 256, "four-wave workgroups");
 #define PASA_K4_LAUNCH(DD, BB)                                                                   \
   hipLaunchKernelGGL((k4_sparse_attn<DD, BB>), grid_video, dim3(K4Cfg<DD, BB>::THREADS), 0, stream, a, \
                      b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal)
   if (rm != nullptr) {  // token-major view of frame-major slices: D = 128, BT = 128 only
     if (D != 128 || BT != 128) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k4_sparse_attn_dma<128, false, true>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b,
-                       cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
-                       n_text_wg, bh, *rm);
-  } else if (D == 128 && BT == 128)
-    hipLaunchKernelGGL((k4_sparse_attn_dma<128, false, false>), grid, dim3(K4D<128>::THREADS), 0, stream, a, b,
-                       cc, pk, selmask, oo, scale, c, T, NT, NG, NW, xcd_chunk, gamma_literal, text, text_valid,
-                       n_text_wg, bh, RowMap{});
-  else if (D == 128 && BT == 64) {
+    if (f16)
+      dma(k4_sparse_attn_dma<128, false, true, false, F16>, grid, xcd_chunk, n_text_wg, *rm);
+    else
+      dma(k4_sparse_attn_dma<128, false, true, false, Bf16>, grid, xcd_chunk, n_text_wg, *rm);
+  } else if (D == 128 && BT == 128) {
+    if (f16)
+      dma(k4_sparse_attn_dma<128, false, false, false, F16>, grid, xcd_chunk, n_text_wg, RowMap{});
+    else
+      dma(k4_sparse_attn_dma<128, false, false, false, Bf16>, grid, xcd_chunk, n_text_wg, RowMap{});
+  } else if (D == 128 && BT == 64) {
     // Query blocks (and text tiles) in pairs: each XCD takes a contiguous run of a
     // slice's pairs.
     const int pair_chunk = ((NT + 1) / 2 + 7) / 8;
     const int n_text_pairs = (bh * ((text_qtiles + 1) / 2) + 7) / 8 * 8;
-    hipLaunchKernelGGL((k4_sparse_attn_dma<64, false, false, true>), dim3(n_text_pairs + 8 * bh * pair_chunk),
-                       dim3(K4D<64, true>::THREADS), 0, stream, a, b, cc, pk, selmask, oo, scale, c, T, NT, NG, NW,
-                       pair_chunk, gamma_literal, text, text_valid, n_text_pairs, bh, RowMap{});
+    const dim3 gp(n_text_pairs + 8 * bh * pair_chunk);
+    if (f16)
+      dma(k4_sparse_attn_dma<64, false, false, true, F16>, gp, pair_chunk, n_text_pairs, RowMap{});
+    else
+      dma(k4_sparse_attn_dma<64, false, false, true, Bf16>, gp, pair_chunk, n_text_pairs, RowMap{});
   }
   else if (D == 64 && BT == 128)
     PASA_K4_LAUNCH(64, 128);
@@ -1148,7 +1163,7 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
 }
 
 hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* o, float scale, int bh,
-                             int T, int text, int text_valid, hipStream_t stream) {
+                             int T, int text, int text_valid, bool f16, hipStream_t stream) {
   constexpr int BT = 128;
   if (T < 1 || text < 0 || text_valid < 0 || text_valid > text) return hipErrorInvalidValue;
   const int NT = (T + BT - 1) / BT;
@@ -1156,9 +1171,15 @@ hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* 
   const int text_qtiles = (text_valid + BT - 1) / BT + (text - text_valid + BT - 1) / BT;
   const int n_text_wg = (bh * text_qtiles + 7) / 8 * 8;
   dim3 grid(n_text_wg + 8 * bh * xcd_chunk);
-  hipLaunchKernelGGL((k4_sparse_attn_dma<BT, true, false>), grid, dim3(K4D<BT>::THREADS), 0, stream,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, nullptr, nullptr, (uint16_t*)o,
-                     scale, scale * kLog2e, T, NT, 0, 0, xcd_chunk, 1, text, text_valid, n_text_wg, bh, RowMap{});
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(K4D<BT>::THREADS), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
+                       (const uint16_t*)v, nullptr, nullptr, (uint16_t*)o, scale, scale * kLog2e, T, NT, 0, 0,
+                       xcd_chunk, 1, text, text_valid, n_text_wg, bh, RowMap{});
+  };
+  if (f16)
+    launch(k4_sparse_attn_dma<BT, true, false, false, F16>);
+  else
+    launch(k4_sparse_attn_dma<BT, true, false, false, Bf16>);
   return hipGetLastError();
 }
 

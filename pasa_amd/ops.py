@@ -58,7 +58,7 @@ def num_selected(density: float, num_blocks: int) -> int:
 @dataclass
 class BlockStats:
     """Outputs of K2.  Statistics fp32: qc/kc/vc [B,H,NT,D], hnorm [B,H,NT], hgroup
-    [B,H,NG,D,D].  With a placement, also the token-major view of q, k, v (bf16, like q),
+    [B,H,NG,D,D].  With a placement, also the token-major view of q, k, v (in q's dtype),
     which the placed attention call reads."""
     qc: torch.Tensor
     kc: torch.Tensor
@@ -191,7 +191,8 @@ def select_from_scores(scores: torch.Tensor, ns: int) -> Selection:
 
 
 def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_tokens: int = 0) -> torch.Tensor:
-    """bf16 phase-2 operands (kbar, V^T, Hbar^T) per (slice, group), as K4 stages them in LDS."""
+    """Phase-2 operands (kbar, V^T, Hbar^T) per (slice, group), in q's dtype (bf16 or
+    fp16), as K4 stages them in LDS."""
     B, H, T, D = q.shape
     lib = _lib.load()
     nbytes = int(lib.pasa_sparse_attn_workspace_bytes(B * H, T, int(text_tokens), D, block_size, GROUP_SIZE))
@@ -200,7 +201,8 @@ def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_t
     pack = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
     _check_device(stats.kc, stats.vc, stats.hgroup)
     _lib.call("pasa_pack_phase2", stats.kc.data_ptr(), stats.vc.data_ptr(), stats.hgroup.data_ptr(),
-              pack.data_ptr(), pack.numel(), B * H, T, int(text_tokens), D, block_size, GROUP_SIZE, _stream(q))
+              pack.data_ptr(), pack.numel(), B * H, T, int(text_tokens), D, block_size, GROUP_SIZE,
+              _DTYPES.get(q.dtype, -1), _stream(q))
     return pack
 
 
@@ -308,7 +310,7 @@ def sparse_attn_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
                     text_tokens: int = 0, text_valid: Optional[int] = None,
                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Dense softmax attention on K4's exact-tile path (bf16, head_dim 128), for the
+    """Dense softmax attention on K4's exact-tile path (bf16 or fp16, head_dim 128), for the
     processors' warm-up layers (reference flash_attention, svg/models/wan/attention.py:299-301,
     svg/models/hyvideo/attention.py:459-476).  With ``text_tokens`` / ``text_valid``
     the attention is block-diagonal over [0, T - text_tokens + text_valid) and the
@@ -345,7 +347,7 @@ def pisa_pg_attention(
 ):
     """PISA with per-group first-order correction (drop-in for reference :307-398).
 
-    q, k, v: [B, H, T, D] contiguous bf16 on a ROCm device; returns o like v.
+    q, k, v: [B, H, T, D] contiguous bf16 (or fp16 at D = 128) on a ROCm device; returns o like v.
     ``timestep``, ``verbose`` and ``prompt_token_length`` do not change the math
     (as in the reference, where ``prompt_token_length`` is documented but unused).
     ``use_random`` adds one N(0,1) draw per key block to the selection score; pass

@@ -100,7 +100,7 @@ def stats(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(q=None), -1), (dict(hg=None), -1), (dict(dtype=2), -7), (dict(dtype=1), -7),
+    (dict(q=None), -1), (dict(hg=None), -1), (dict(dtype=2), -7), (dict(dtype=1, D=64), -7), (dict(dtype=5), -7),
     (dict(D=96), -3), (dict(BT=32), -4), (dict(T=0), -2), (dict(bh=-1), -2), (dict(G=0), -12),
     (dict(T=1 << 31), -6), (dict(T=(1 << 24) - 100), -6),
     (dict(text=-1), -10), (dict(text=1000), -10), (dict(text=10, D=64), -10),
@@ -155,7 +155,7 @@ def attn(lib, **kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(o=None), -1), (dict(mask=None), -1), (dict(idx=None, mask=None), -1), (dict(idx=None, D=256), -3),
-    (dict(dtype=2), -7), (dict(D=256), -3),
+    (dict(dtype=2), -7), (dict(dtype=1, D=64, BT=64), -7), (dict(D=256), -3),
     (dict(BT=256), -4), (dict(G=16), -12), (dict(ns=0), -5), (dict(ns=9), -5),
     (dict(scale=0.0), -9), (dict(scale=-1.0), -9), (dict(scale=float("nan")), -9),
     (dict(lit=2), -9), (dict(ws=None), -8), (dict(wsb=10), -8), (dict(T=0), -2),
@@ -209,10 +209,13 @@ def test_noalloc_scratch_limit_matches_header(lib):
 def test_packed_entry_validation(lib):
     pk = lib.pasa_pack_phase2
     need = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 0, 128, 128, 32)
-    assert pk(FAKE, FAKE, FAKE, FAKE, need - 1, 2, 1000, 0, 128, 128, 32, None) == -8
-    assert pk(None, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 32, None) == -1
-    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 16, None) == -12
-    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 1000, 128, 128, 32, None) == -10
+    assert pk(FAKE, FAKE, FAKE, FAKE, need - 1, 2, 1000, 0, 128, 128, 32, 0, None) == -8
+    assert pk(None, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 32, 0, None) == -1
+    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 16, 0, None) == -12
+    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 1000, 128, 128, 32, 0, None) == -10
+    assert pk(FAKE, FAKE, FAKE, FAKE, need, 2, 1000, 0, 128, 128, 32, 2, None) == -7    # fp32 pack
+    need64 = lib.pasa_sparse_attn_workspace_bytes(2, 1000, 0, 64, 64, 32)
+    assert pk(FAKE, FAKE, FAKE, FAKE, need64, 2, 1000, 0, 64, 64, 32, 1, None) == -7    # fp16 needs D 128
     f = lib.pasa_sparse_attn_packed
     args = [FAKE, FAKE, FAKE, FAKE, need, FAKE, FAKE, FAKE, 0.1, 2, 1000, 0, 0, 128, 128, 32, 2, 1, 0, None]
     bad = list(args); bad[4] = 0

@@ -40,14 +40,15 @@ def say(msg):
     sys.stdout.flush()
 
 
-def check_parity(out, ref, what, floor=None):
-    """cos >= 0.999, and the error beyond one bf16 ulp <= 2e-2 * RMS.  With ``floor``
-    (the metrics of the reference-precision oracle against the same fp32 reference):
-    max|err| <= 1.5 x the floor's + one ulp, and the excess bound is max(2e-2, 1.5 x the
-    floor's excess) * RMS -- where the reference's own bf16 roundings already exceed
-    2e-2 * RMS beyond one ulp (at the HunyuanVideo shape, near-zero outputs that come from
-    cancelling sums), the kernel is held to that floor instead."""
-    m = O.parity_metrics(out, ref)
+def check_parity(out, ref, what, floor=None, dtype=torch.bfloat16):
+    """cos >= 0.999, and the error beyond one ulp of the output type ``dtype`` (bf16 or
+    fp16) <= 2e-2 * RMS.  With ``floor`` (the metrics of the reference-precision oracle
+    against the same fp32 reference): max|err| <= 1.5 x the floor's + one ulp, and the
+    excess bound is max(2e-2, 1.5 x the floor's excess) * RMS -- where the reference's own
+    roundings already exceed 2e-2 * RMS beyond one ulp (at the HunyuanVideo shape,
+    near-zero outputs that come from cancelling sums), the kernel is held to that floor
+    instead."""
+    m = O.parity_metrics(out, ref, dtype)
     say(f"[parity] {what}: cos={m['cos']:.7f} max_abs/rms={m['max_abs_over_rms']:.3e} "
         f"excess/rms={m['excess_over_rms']:.3e}"
         + ("" if floor is None else f" floor max_abs/rms={floor['max_abs_over_rms']:.3e} "
@@ -56,7 +57,7 @@ def check_parity(out, ref, what, floor=None):
     bound = EXCESS_OVER_RMS if floor is None else max(EXCESS_OVER_RMS, 1.5 * floor["excess_over_rms"])
     assert m["excess_over_rms"] <= bound, (what, m, floor)
     if floor is not None:
-        ulp = float(O.bf16_ulp(torch.tensor(ref.abs().max().item())))
+        ulp = float(O.ulp(torch.tensor(ref.abs().max().item()), dtype))
         assert m["max_abs"] <= 1.5 * floor["max_abs"] + ulp, (what, m, floor)
     return m
 
@@ -610,6 +611,102 @@ def test_processor_dense_split_matches_two_sdpa_calls(device):
                      torch.nn.functional.scaled_dot_product_attention(q[:, :, 421:].float(), k[:, :, 421:].float(),
                                                                        v[:, :, 421:].float())], dim=2).cpu()
     check_parity(o, ref.double(), "processor dense split")
+
+
+# ------------------------------------------------------------------ fp16 ------
+# The D = 128 path takes fp16 q, k, v as well: the statistics stay fp32, P, the phase-2
+# pack and the output are fp16 (the reference casts P to v's dtype and stores its
+# statistics and output in it).  The floor is the oracle at fp16 precision.
+
+def f16_inputs(heads, grid, BT, seed=0, density=0.15, text=0):
+    base = WORKLOADS["c3"] if text else WORKLOADS["c1"]
+    wl = small_workload(base, heads=heads, grid=grid, block_size=BT, density=density, text_tokens=text,
+                        prescale=1.0, scale=None)
+    return wl, make_inputs(wl, seed=seed, dtype=torch.float16)
+
+
+@pytest.mark.parametrize("heads,grid,BT", [(2, (3, 10, 20), 128), (1, (9, 45, 80), 64), (1, (21, 30, 52), 128)])
+def test_block_stats_f16(device, heads, grid, BT):
+    wl, (q, k, v) = f16_inputs(heads, grid, BT)
+    T = wl.seq_len
+    say(f"[K2 fp16] heads={heads} T={T} BT={BT}")
+    st = ops.block_stats(q.to(device), k.to(device), v.to(device), BT, 32)
+    ref = O.block_stats(*(t.reshape(heads, T, 128) for t in (q, k, v)), BT, dtype=torch.float64)
+    hg = O.group_moment(ref.hc, 32)
+    for name, got, exp, rtol in (("qc", st.qc, ref.qc, 2e-5), ("kc", st.kc, ref.kc, 2e-5), ("vc", st.vc, ref.vc, 2e-5),
+                                 ("hnorm", st.hnorm, ref.hnorm, 1e-4), ("hgroup", st.hgroup, hg, 1e-4)):
+        got = got.cpu().double().reshape(exp.shape)
+        tol = rtol * float(exp.abs().max()) + 1e-6
+        err = float((got - exp).abs().max())
+        say(f"[K2 fp16]   {name}: max err {err:.3e} (tol {tol:.3e})")
+        assert err <= tol, name
+
+
+@pytest.mark.parametrize("heads,grid,BT,density,gamma,text,valid", [
+    (2, (3, 10, 20), 128, 0.4, "literal", 0, None),        # ragged last block
+    (1, (9, 45, 80), 64, 0.1, "literal", 0, None),         # block 64: query-block pairs, the last a repeat
+    (2, (21, 30, 52), 128, 0.15, "consistent", 0, None),   # c1 shape
+    (1, (3, 10, 20), 128, 0.4, "literal", 256, 77),        # text segment with padding
+    (1, (3, 10, 20), 64, 0.4, "literal", 40, None),        # text segment at block 64
+])
+def test_sparse_attn_f16(device, heads, grid, BT, density, gamma, text, valid):
+    wl, (q, k, v) = f16_inputs(heads, grid, BT, seed=5, density=density, text=text)
+    say(f"[K4 fp16] heads={heads} T={wl.seq_len} text={text} valid={valid} BT={BT} density={density} {gamma}")
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    scale = 128 ** -0.5
+    st = ops.block_stats(qd, kd, vd, BT, 32, text_tokens=text)
+    sel = ops.select_blocks(st, density, scale)
+    o = ops.sparse_attn(qd, kd, vd, st, sel, scale, BT, gamma, text_tokens=text, text_valid=valid)
+    assert o.dtype == torch.float16
+    kw = dict(gamma=gamma, indices=sel.idx.cpu(), text_tokens=text, text_valid=valid)
+    ref = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, **kw)
+    rp = O.pisa_pg_attention(q, k, v, density, BT, 32, scale, ref_precision=torch.float16, **kw)
+    floor = O.parity_metrics(rp, ref, torch.float16)
+    check_parity(o.cpu(), ref, f"K4 fp16 {wl.seq_len}x128 BT{BT} text {text} {gamma}", floor, torch.float16)
+    # fp16 carries three more significand bits than bf16: the same selection run on the
+    # bf16 roundings of the inputs is further off
+    qb, kb, vb = qd.bfloat16(), kd.bfloat16(), vd.bfloat16()
+    stb = ops.block_stats(qb, kb, vb, BT, 32, text_tokens=text)
+    ob = ops.sparse_attn(qb, kb, vb, stb, sel, scale, BT, gamma, text_tokens=text, text_valid=valid)
+    e16 = (o.cpu().double() - ref.double()).abs().max().item()
+    e_bf = (ob.cpu().double() - ref.double()).abs().max().item()
+    say(f"[K4 fp16]   max err fp16 {e16:.3e}, bf16 {e_bf:.3e}")
+    assert e16 < e_bf
+
+
+def test_dense_attention_f16(device):
+    heads, T, text, valid = 2, 1000, 100, 37
+    g = torch.Generator().manual_seed(17)
+    q, k, v = (torch.randn(1, heads, T, 128, generator=g).to(torch.float16) for _ in range(3))
+    o = ops.dense_attention(q.to(device), k.to(device), v.to(device), text_tokens=text, text_valid=valid).cpu()
+    assert o.dtype == torch.float16
+    es = O.effective_scale(128 ** -0.5)
+    seg = T - text + valid
+    qd, kd, vd = q.double(), k.double(), v.double()
+    ref = torch.empty(1, heads, T, 128, dtype=torch.float64)
+    ref[..., :seg, :] = O.dense_attention(qd[..., :seg, :], kd[..., :seg, :], vd[..., :seg, :], es)
+    ref[..., seg:, :] = O.dense_attention(qd[..., seg:, :], kd[..., seg:, :], vd[..., seg:, :], es)
+    rp = O.pisa_pg_attention(q.float(), k.float(), v.float(), 1.0, 128, 32, 128 ** -0.5,
+                             ref_precision=torch.float16, text_tokens=text, text_valid=valid)
+    floor = O.parity_metrics(rp, ref, torch.float16)
+    check_parity(o, ref, f"dense fp16 T={T} text={text} valid={valid}", floor, torch.float16)
+
+
+def test_placed_attention_f16_equals_permute_attend_unpermute(device):
+    from pasa_amd import placement as PL
+    F, P, text, H, D, density = 5, 200, 40, 2, 128, 0.3
+    T = F * P + text
+    g = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(1, H, T, D, generator=g).to(torch.float16).to(device) for _ in range(3))
+    fl = torch.tensor([[1, 0]], dtype=torch.int32, device=device)
+    o = ops.pisa_pg_attention(q, k, v, density, block_size=128, text_tokens=text, placement=ops.Placement(F, P, fl))
+    qs, ks, vs = (torch.empty_like(t) for t in (q, k, v))
+    PL.hunyuan_sparse_head_placement(q, k, v, qs, ks, vs, fl, text, F, P)
+    ot = ops.pisa_pg_attention(qs, ks, vs, density, block_size=128, text_tokens=text)
+    ref = torch.empty_like(ot)
+    PL.hunyuan_hidden_states_placement(ot, ref, fl, text, F, P)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float16 and torch.equal(o, ref)
 
 
 # ---------------------------------------------------- placement folded in --

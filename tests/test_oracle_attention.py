@@ -310,3 +310,37 @@ def test_reference_precision_text_rows_round_p():
     want = ((pb @ v[0, 0]) / p.sum(-1, keepdim=True)).to(torch.bfloat16).to(f64)
     torch.testing.assert_close(out[0, 0, T - X:], want, rtol=0, atol=0)
     assert not torch.equal(pb, p)
+
+
+@pytest.mark.parametrize("dtype,fn", [(torch.bfloat16, O.bf16_ulp), (torch.float16, O.f16_ulp)])
+def test_ulp_is_the_spacing_of_adjacent_values(dtype, fn):
+    """ulp(x) = next representable value above |x| minus |x|, over normal and (fp16)
+    subnormal magnitudes, from the bit patterns themselves."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(4000, generator=g, dtype=f64) * torch.exp2(torch.randint(-30, 12, (4000,), generator=g))).to(dtype)
+    x = x[torch.isfinite(x) & (x != 0)].abs()
+    nxt = (x.view(torch.int16) + 1).view(dtype)
+    ok = torch.isfinite(nxt)
+    spacing = nxt[ok].double() - x[ok].double()
+    torch.testing.assert_close(fn(x[ok].double()), spacing, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_reference_precision_rounds_to_the_requested_type(dtype):
+    """ref_precision=dtype: every output is representable in dtype, and it differs from
+    the unrounded oracle by no more than the roundings of P, the statistics and the
+    output can account for (a few ulps of dtype relative to the output scale)."""
+    q, k, v = rand_qkv(1, 2, 200, 16, seed=9, scale=1.0)
+    s = 16 ** -0.5
+    exact, aux = O.pisa_pg_attention(q, k, v, 0.3, 16, 4, s, dtype=f64, return_aux=True)
+    idx = aux["idx"].reshape(1, 2, -1, aux["idx"].shape[-1])
+    rp = O.pisa_pg_attention(q, k, v, 0.3, 16, 4, s, dtype=f64, indices=idx, ref_precision=dtype)
+    assert torch.equal(rp, rp.to(dtype).to(f64))
+    err = (rp - exact).abs().max().item()
+    scale = exact.abs().max().item()
+    eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    assert 0 < err <= 16 * eps * scale
+    # fp16 keeps more bits than bf16, so its emulation lands closer to the exact oracle
+    if dtype == torch.float16:
+        rb = O.pisa_pg_attention(q, k, v, 0.3, 16, 4, s, dtype=f64, indices=idx, ref_precision=True)
+        assert err < (rb - exact).abs().max().item()
