@@ -44,7 +44,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-dit", action="store_true", help="skip the c4 DiT denoising-step sweep")
     ap.add_argument("--no-other-configs", action="store_true",
-                    help="skip the c1 / c3 / c2-at-block-64 step timings")
+                    help="skip the c1 / c3 / block-64 / c2-in-fp16 step timings")
     ap.add_argument("--dit-steps", type=int, default=2, help="timed denoising steps per c4 variant")
     args = ap.parse_args()
 
@@ -261,7 +261,8 @@ def main() -> int:
         others = {}
         for name, w in (("c1", WORKLOADS["c1"]), ("c3", WORKLOADS["c3"]),
                         ("c2_block64", dataclasses.replace(wl, block_size=64)),
-                        ("c3_block64", dataclasses.replace(WORKLOADS["c3"], block_size=64))):
+                        ("c3_block64", dataclasses.replace(WORKLOADS["c3"], block_size=64)),
+                        ("c2_fp16", dataclasses.replace(wl, dtype=torch.float16))):
             others[name] = config_step(torch, ops, make_inputs, w, dev, args.seed)
             log(f"{name}: {others[name]['ms_per_step']:.3f} ms/step, {others[name]['TFLOPs_effective']:.1f} "
                 f"TFLOP/s effective, K4 {others[name]['k4_ms']:.3f} ms")
@@ -420,7 +421,7 @@ def config_step(torch, ops, make_inputs, wl, dev, seed: int, steps: int = 10, wa
     k3 = statistics.mean(e[3].elapsed_time(e[0]) for e in ev)
     k2 = statistics.mean(e[2].elapsed_time(e[3]) for e in ev)
     res = {"workload": f"{wl.name}: H={wl.heads} T={wl.seq_len} D={wl.head_dim} block {BT} density {wl.density} "
-                       f"NS={ns}" + (f" text {X}" if X else ""),
+                       f"NS={ns}" + (f" text {X}" if X else "") + f" {str(wl.dtype).replace('torch.', '')}",
            "ms_per_step": round(ms, 4), "k4_ms": round(k4, 4), "k4_TFLOPs": round(flops / k4 / 1e9, 1),
            "k3_ms": round(k3, 4), "k2_and_pack_ms": round(k2, 4),
            "TFLOPs_effective": round(flops / ms / 1e9, 1), "flops": flops}

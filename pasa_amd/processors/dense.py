@@ -3,7 +3,7 @@
 (svg/models/wan/attention.py:299-301, :378-379; svg/models/hyvideo/attention.py:450-476,
 :509-510, :632-633, :671-672).
 
-bf16 device tensors with head_dim 128 run on K4's exact-tile path
+bf16 or fp16 device tensors with head_dim 128 run on K4's exact-tile path
 (``pasa_amd.ops.dense_attention``, 1.6x PyTorch SDPA at the Wan-14B 720p shape).
 Other inputs (fp32 models, other head dims, the CPU tensors of the processor unit
 tests) take PyTorch SDPA, as the reference does.
@@ -19,7 +19,7 @@ from .. import ops
 
 
 def kernel_ok(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> bool:
-    return (query.is_cuda and query.dtype == torch.bfloat16 and query.shape[-1] == 128
+    return (query.is_cuda and query.dtype in (torch.bfloat16, torch.float16) and query.shape[-1] == 128
             and query.shape == key.shape == value.shape and key.dtype == value.dtype == query.dtype)
 
 
