@@ -6,9 +6,8 @@
 //
 // One workgroup (4 wavefronts) owns one group of G consecutive key blocks of one
 // (batch, head) slice and walks its blocks in order.  Per block it streams the
-// Q, K, V tiles from HBM once, forms the column sums with in-register partials
-// reduced by shuffles and LDS (fixed order, deterministic), computes
-// H_j = K_j^T V_j on bf16 MFMA (each wave owns one quadrant of the D x D
+// Q, K, V tiles from HBM once, forms the column sums (fixed order, deterministic),
+// computes H_j = K_j^T V_j on the MFMA (each wave owns one quadrant of the D x D
 // matrix), subtracts kc vc^T, reduces ||H_j||_F and adds H_j into the group
 // accumulator held in registers.  H_j is never written to memory; the group
 // mean is written once per group.  All statistics are fp32.
@@ -218,11 +217,15 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 // tiles go straight into double-buffered LDS (direct loads, 256-byte rows with 16-byte
 // chunk c of row r at c ^ 4(r & 3)); Q rows go to registers.  Block j+1's loads are in
 // flight while block j is reduced.  H_j = K^T V reads both MFMA operands with the
-// transposing ds_read_b64_tr_b16 (K^T as A, V as B; the same token order in both).
+// transposing ds_read_b64_tr_b16 (K^T as A, V as B; the same token order in both); the K
+// and V column sums are two more MFMAs per step against a ones operand, and the Q column
+// sums are per-thread sums of its Q rows.  The Q sums and ||H_j||^2 reach LDS as per-wave
+// partials that the next block's barrier publishes (one workgroup barrier per block).
 // PERM: q, k, v are frame-major; the statistics are those of their token-major view (rm),
 // and the token-major view itself is written to qt, kt, vt: each row of a block goes out
-// from the registers (Q) and LDS tiles (K, V) the column sums read it from, and the
-// workgroup of group 0 copies the text rows [T, Tslice), which stay in place.
+// from the registers (Q) and the LDS tiles (K, V), and the workgroup of group 0 copies
+// the text rows [T, Tslice), which stay in place.
+// E: the 16-bit element type of q, k, v (Bf16 or F16).
 // BT 128 (two 64 KB buffer pairs: one workgroup per CU) or 64 (two per CU).
 template <int BT, bool PERM, typename E = Bf16>
 __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(

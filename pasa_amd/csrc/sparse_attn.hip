@@ -13,7 +13,7 @@
 // MI355X mapping.  One workgroup = one (slice, query block) of BT rows; one
 // wavefront per 32 query rows.  Everything is computed transposed so that a lane
 // owns one query (lane % 32) and the softmax statistics are per-lane scalars:
-//   S^T[key][q]  = K  * Q^T   (v_mfma_f32_32x32x16_bf16, K from LDS, Q in VGPRs)
+//   S^T[key][q]  = K  * Q^T   (v_mfma_f32_32x32x16_bf16 or _f16, K from LDS, Q in VGPRs)
 //   O^T[e][q]   += V^T * P^T   (V^T read from the row-major V tile with
 //                               ds_read_b64_tr_b16, P from the S^T accumulators)
 // The S^T accumulator of a lane holds, per 16-key step s, exactly the 8 keys
@@ -42,8 +42,10 @@
 // instruction issues only between the MFMAs of the SIMD's other wave, so it stalls
 // its wave behind the partner's MFMA stream).
 //
-// Phase-2 operands (kbar, V^ transposed, Hbar transposed; bf16) are packed per
-// (slice, group) by k4_pack / k4_pack_xor into the exact LDS image K4 copies in.
+// Phase-2 operands (kbar, V^ transposed, Hbar transposed; in the input's 16-bit type) are
+// packed per (slice, group) by k4_pack / k4_pack_xor into the exact LDS image K4 copies in.
+// The D = 128 kernels and k4_pack_xor take that type as a template argument (Bf16 or
+// F16: the MFMA and the rounding of P, the pack and o); the D = 64 ones are bf16.
 #include "common.h"
 #include "kernels.h"
 
