@@ -522,10 +522,11 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
 // tiles never pass through VGPRs: buffer_load_dwordx4 ... lds writes each lane's
 // 16 bytes to LDS directly (zeros past the end of the slice), which frees the
 // staging registers for deeper LDS-operand prefetching while two workgroups
-// still share each CU.  Per block i, with one K and one V buffer:
-//   wait K_i -> barrier -> S = K_i Q^T -> wait V_i -> barrier -> load K_{i+1}
-//   -> softmax -> O += V_i P -> barrier -> load V_{i+1}
-// so K_{i+1} streams in during softmax + P.V and V_{i+1} during the next S.
+// still share each CU.  Per block i, with one K and one V buffer, two barriers:
+//   wait K_i -> barrier -> load V_i -> S = K_i Q^T -> softmax
+//   -> wait V_i -> barrier -> load K_{i+1} -> O += V_i P
+// Each barrier both publishes a landed tile and frees the other buffer, so V_i
+// streams in during S + softmax and K_{i+1} during P.V.
 // Tiles use 256-byte rows with XOR-swizzled 16-byte chunks: K chunk c of row r
 // sits at c ^ (r & 15) (conflict-free MFMA A-operand reads of 16 rows), V chunk
 // c at c ^ 4*(r & 3) (conflict-free transposing reads).  The phase-2 pack image
@@ -776,15 +777,13 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   }
   int nv_cur = 0;
   int blk = next_tile(nv_cur);
-  if (blk >= 0) {
-    load_k(blk);
-    load_v(blk);
-  }
+  if (blk >= 0) load_k(blk);
   while (blk >= 0) {
     int nv_nxt = 0;
     const int nxt = next_tile(nv_nxt);
-    wait_vmcnt<C::TILE_LOADS>();  // this wave's K_blk loads landed (V_blk may be in flight)
-    barrier_lds_reads_done();     // ... and every wave's
+    wait_vmcnt<0>();           // this wave's K_blk loads landed
+    barrier_lds_reads_done();  // ... and every wave's; every wave is done reading the V buffer
+    load_v(blk);
 
     f32x16_t sacc[BT / 32];
 #pragma unroll
@@ -812,9 +811,6 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
 #pragma unroll
       for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
     }
-
-    barrier_lds_reads_done();  // every wave is done reading K_blk
-    if (nxt >= 0) load_k(nxt);
 
     const int nvalid = nv_cur;
     if (nvalid < BT) {
@@ -860,13 +856,10 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       pf[s] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
     }
     l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
-    // V_blk is waited for only now, so its load overlaps S and the softmax; the
-    // K_{blk+1} loads issued after it may stay in flight.
-    if (nxt >= 0)
-      wait_vmcnt<C::TILE_LOADS>();
-    else
-      wait_vmcnt<0>();
-    barrier_lds_reads_done();  // every wave's part of V_blk landed
+    // V_blk is waited for only now, so its load overlaps S and the softmax.
+    wait_vmcnt<0>();
+    barrier_lds_reads_done();  // every wave's part of V_blk landed; every wave is done reading K_blk
+    if (nxt >= 0) load_k(nxt);
 #pragma unroll
     for (int s = 0; s < BT / 16; ++s)
 #pragma unroll
@@ -889,8 +882,6 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
     }
-    barrier_lds_reads_done();  // every wave is done reading V_blk
-    if (nxt >= 0) load_v(nxt);
     blk = nxt;
     nv_cur = nv_nxt;
     if (PAIR) ++tiles_done;
@@ -898,8 +889,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   if (PAIR) {
     for (; tiles_done < pair_tiles; ++tiles_done)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) barrier_lds_reads_done();  // the loop's four barriers per tile
+      for (int b = 0; b < 2; ++b) barrier_lds_reads_done();  // the loop's barriers per tile
   }
+  barrier_lds_reads_done();  // every wave is done reading the V buffer
 
   // ---------------- Phase 2 ------------------------------------------------------
   const int last_len = T - (NT - 1) * BT;
