@@ -137,7 +137,7 @@ class HunyuanVideoAttnProcessor2_0_FlashAttention:
     def __init__(self, layer_idx):
         self.layer_idx = layer_idx
         if not hasattr(F, "scaled_dot_product_attention"):
-            raise ImportError("HunyuanVideoAttnProcessor2_0_FlashAttention requires PyTorch 2.0.")
+            raise ImportError("the HunyuanVideo processors need torch.nn.functional.scaled_dot_product_attention (PyTorch >= 2.0)")
 
     fused_prologue = True
 
@@ -209,7 +209,7 @@ class Hunyuan_SVGAttn_Processor2_0:
     def __init__(self, layer_idx):
         self.layer_idx = layer_idx
         if not hasattr(F, "scaled_dot_product_attention"):
-            raise ImportError("Hunyuan_SparseAttn requires PyTorch 2.0, please upgrade PyTorch.")
+            raise ImportError("the HunyuanVideo processors need torch.nn.functional.scaled_dot_product_attention (PyTorch >= 2.0)")
 
     def get_qkv(self, attn, hidden_states):
         return attn.to_q(hidden_states), attn.to_k(hidden_states), attn.to_v(hidden_states)
@@ -341,10 +341,10 @@ class Hunyuan_PASA_Processor(Hunyuan_SVGAttn_Processor2_0):
 
     def attention_core_logic(self, query, key, value, timestep, layer_idx, cu_max_seqlens):
         cfg, num_heads, seq_len, dim = query.size()
-        assert cfg == 1, "Batch size must be 1 for kmeans block sparse attention"
+        assert cfg == 1, f"the sparse path attends one sample per call, got a batch of {cfg}"
         context_length, num_frame, frame_size = self.context_length, self.num_frame, self.frame_size
         assert seq_len == context_length + num_frame * frame_size, (
-            f"Query Shape: {seq_len} is not equivalent to {context_length} + {num_frame} * {frame_size}")
+            f"{seq_len} tokens, expected {context_length} text + {num_frame} frames x {frame_size}")
 
         full_attention_flag = False
         if self.layer_idx < self.first_layers_fp:
@@ -358,7 +358,7 @@ class Hunyuan_PASA_Processor(Hunyuan_SVGAttn_Processor2_0):
 
         ts = int(timestep[0].item()) if torch.is_tensor(timestep[0]) else int(timestep[0])
         density = _density.lookup_rescaled_density(self.rescaled_density, ts)
-        assert density is not None, f"Density is not found for timestep {ts}"
+        assert density is not None, f"no density is scheduled for timestep {ts}"
         if not self.use_group:
             raise NotImplementedError("use_group=False selects piecewise_sparse_attention "
                                       "(svg/kernels/triton/pisa_attention.py), which this build does not provide")
@@ -425,5 +425,5 @@ def replace_hyvideo_attention(pipe, height, width, num_frames, prompt_length, fi
         for layer_idx, m in enumerate(pipe.transformer.single_transformer_blocks):
             m.attn.processor = M(layer_idx=layer_idx + n_double)
     elif pattern != "dense":
-        raise ValueError(f"Invalid pattern: {pattern}")
+        raise ValueError(f"unknown attention pattern {pattern!r} (expected 'PASA' or 'dense')")
     return width / frame_size

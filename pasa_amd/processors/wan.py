@@ -51,7 +51,7 @@ class WanAttn_SVGAttn_Processor2_0:
     def __init__(self, layer_idx):
         self.layer_idx = layer_idx
         if not hasattr(F, "scaled_dot_product_attention"):
-            raise ImportError("WanAttnProcessor2_0 requires PyTorch 2.0.")
+            raise ImportError("the Wan processors need torch.nn.functional.scaled_dot_product_attention (PyTorch >= 2.0)")
 
     def get_qkv(self, attn, hidden_states, encoder_hidden_states):
         return attn.to_q(hidden_states), attn.to_k(encoder_hidden_states), attn.to_v(encoder_hidden_states)
@@ -61,11 +61,11 @@ class WanAttn_SVGAttn_Processor2_0:
         # rmsnorm's single rounding (reference :122-136).
         if attn.norm_q is not None:
             if not is_rmsnorm(attn.norm_q):
-                raise ValueError(f"Unsupported norm type: {type(attn.norm_q)}")
+                raise ValueError(f"norm_q is {type(attn.norm_q).__name__}; only RMSNorm is handled")
             query = rms_norm_once(query, attn.norm_q.weight, norm_eps(attn.norm_q, query.dtype))
         if attn.norm_k is not None:
             if not is_rmsnorm(attn.norm_k):
-                raise ValueError(f"Unsupported norm type: {type(attn.norm_k)}")
+                raise ValueError(f"norm_k is {type(attn.norm_k).__name__}; only RMSNorm is handled")
             key = rms_norm_once(key, attn.norm_k.weight, norm_eps(attn.norm_k, key.dtype))
         return query, key
 
@@ -191,10 +191,10 @@ class Wan_PASA_Processor(WanAttn_SVGAttn_Processor2_0):
 
     def attention_core_logic(self, query, key, value, timestep):
         cfg, num_heads, seq_len, dim = query.size()
-        assert cfg == 1, "Batch size must be 1 for kmeans block sparse attention"
+        assert cfg == 1, f"the sparse path attends one sample per call, got a batch of {cfg}"
         context_length, num_frame, frame_size = self.context_length, self.num_frame, self.frame_size
         assert seq_len == context_length + num_frame * frame_size, (
-            f"Query Shape: {seq_len} is not equivalent to {context_length} + {num_frame} * {frame_size}")
+            f"{seq_len} tokens, expected {context_length} text + {num_frame} frames x {frame_size}")
 
         full_attention_flag = False
         if self.layer_idx < self.first_layers_fp:
@@ -208,7 +208,7 @@ class Wan_PASA_Processor(WanAttn_SVGAttn_Processor2_0):
 
         ts_key = int(timestep[0].item()) if torch.is_tensor(timestep[0]) else int(timestep[0])
         density = self.rescaled_density.get(ts_key)
-        assert density is not None, f"Density is not found for timestep {ts_key}"
+        assert density is not None, f"no density is scheduled for timestep {ts_key}"
         out = pisa_pg_attention(query.contiguous(), key.contiguous(), value.contiguous(),
                                 density=density, block_size=self.block_size,
                                 use_random=self.use_random)
@@ -238,7 +238,7 @@ def replace_wan_attention(pipe, height, width, num_frames, first_layers_fp, firs
     num_layers = len(pipe.transformer.blocks)
 
     if pattern != "PASA":
-        raise ValueError(f"Pattern '{pattern}' not supported")
+        raise ValueError(f"unknown attention pattern {pattern!r} (expected 'PASA')")
     if logging_file is not None:
         os.makedirs(os.path.dirname(logging_file) or ".", exist_ok=True)
         with open(logging_file, "w") as f:
@@ -258,4 +258,4 @@ def replace_wan_attention(pipe, height, width, num_frames, first_layers_fp, firs
     for layer_idx, m in enumerate(pipe.transformer.blocks):
         if hasattr(m.attn1, "processor"):
             m.attn1.set_processor(AttnModule(layer_idx=layer_idx))
-    print(f"Attention processors replaced with {pattern} pattern.")
+    print(f"[pasa_amd] {pattern} processors installed on {num_layers} attention layers")
