@@ -46,6 +46,8 @@ def main() -> int:
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the c1 / c3 / block-64 / c2-in-fp16 step timings")
     ap.add_argument("--dit-steps", type=int, default=2, help="timed denoising steps per c4 variant")
+    ap.add_argument("--power-probe", action="store_true",
+                    help="run only the K4 power probe (real vs all-zero operands) and print its JSON")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -74,6 +76,13 @@ def main() -> int:
     q, k, v = (t.to(dev) for t in make_inputs(wl, seed=args.seed))
     torch.cuda.synchronize()
     log(f"inputs ready in {time.perf_counter() - t0:.1f}s")
+
+    if args.power_probe:
+        st = ops.block_stats(q, k, v, BT, 32, text_tokens=X)
+        pack = ops.pack_phase2(q, st, BT, X)
+        sel = ops.select_blocks(st, wl.density, scale, indices=False)
+        print(json.dumps({"k4_power_probe": power_probe(torch, ops, q, k, v, pack, sel, wl)}), flush=True)
+        return 0
 
     out = torch.empty_like(v)
     last_sel = []
@@ -117,6 +126,10 @@ def main() -> int:
     value = flops_k4 / (ms_per_step * 1e-3) / 1e12
     log(f"ms/step {ms_per_step:.3f}  K2 {k2_only:.3f} + pack {pack_ms:.3f}  K3 {k3:.3f}  K4 {k4:.3f} ms  "
         f"-> {value:.1f} TFLOP/s effective, K4 {achieved:.1f} TFLOP/s")
+
+    probe = power_probe(torch, ops, q, k, v, ops.pack_phase2(q, last_sel[1], BT, X), last_sel[0], wl)
+    log(f"K4 power probe: real operands {probe['k4_real_ms']:.3f} ms, all-zero operands "
+        f"{probe['k4_zero_operands_ms']:.3f} ms (x{probe['real_over_zero']:.3f})")
 
     # K1: frame-major <-> token-major permutation of Q, K, V (forward) and O (inverse).
     F, Hh, W = wl.grid
@@ -383,11 +396,38 @@ def main() -> int:
         "k6_row_ops": {"ms": round(k6_ms, 4), "GBps": round(k6_gbps, 1), "bytes": k6_bytes,
                        "frac_of_hbm_peak": round(k6_gbps / PEAK_HBM_GBPS, 4),
                        "mode": "h = bf16(h + x*gate) in place, y = LayerNorm(h)*w + b, 75600 x 5120 bf16"},
+        "k4_power_probe": probe,
         "other_configs": others,
         "c4_dit_step": dit,
     }
     print(json.dumps(res), flush=True)
     return 0
+
+
+def power_probe(torch, ops, q, k, v, pack, sel, wl, reps: int = 4) -> dict:
+    """K4 on one selection and launch shape twice: with the real q, k, v and phase-2 pack,
+    and with all four replaced by zeros of the same shapes.  The instruction stream, the
+    tiles each workgroup loads and so the memory traffic are identical; only the operand
+    values differ.  Four real launches, then four zero-operand launches (after one warm-up
+    launch of each), so a profile of this run tells them apart by dispatch order."""
+    BT, X = wl.block_size, wl.text_tokens
+    zq, zk, zv, zp = (torch.zeros_like(t) for t in (q, k, v, pack))
+    out = torch.empty_like(v)
+    res = {}
+    for name, args in (("real", (q, k, v, pack)), ("zero", (zq, zk, zv, zp))):
+        ops.sparse_attn_packed(*args, sel, wl.op_scale, BT, out=out, text_tokens=X)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in ev:
+            e0.record()
+            ops.sparse_attn_packed(*args, sel, wl.op_scale, BT, out=out, text_tokens=X)
+            e1.record()
+        torch.cuda.synchronize()
+        res[name] = statistics.median(e0.elapsed_time(e1) for e0, e1 in ev)
+    del zq, zk, zv, zp, out
+    return {"k4_real_ms": round(res["real"], 4), "k4_zero_operands_ms": round(res["zero"], 4),
+            "real_over_zero": round(res["real"] / res["zero"], 4),
+            "note": "same selection, launch and tile loads; operands all zero in the second: the time "
+                    "difference is the clock the chip holds under each (power limit), not work"}
 
 
 def config_step(torch, ops, make_inputs, wl, dev, seed: int, steps: int = 10, warmup: int = 3) -> dict:
