@@ -47,6 +47,31 @@ def _check_device(*ts: torch.Tensor) -> None:
             raise ValueError("PISA kernels need contiguous tensors")
 
 
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """q, k, v: one [B, H, T, D] shape and one dtype (the kernels index k and v with q's
+    sizes and read all three as q's element type)."""
+    if q.dim() != 4:
+        raise ValueError(f"q, k, v must be [B, H, T, D], got {tuple(q.shape)}")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q, k, v must have one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+
+
+def _check_stats(stats: "BlockStats", q: torch.Tensor, block_size: int, text_tokens: int) -> None:
+    """The statistics must be block_stats' for q's shape and this block size: the pack
+    kernel reads kc, vc and hgroup with the sizes derived from q."""
+    B, H, T, D = q.shape
+    NT = math.ceil((T - int(text_tokens)) / block_size)
+    NG = math.ceil(NT / GROUP_SIZE)
+    want = {"kc": (B, H, NT, D), "vc": (B, H, NT, D), "hgroup": (B, H, NG, D, D)}
+    for name, shape in want.items():
+        t = getattr(stats, name)
+        if tuple(t.shape) != shape or t.dtype != torch.float32:
+            raise ValueError(f"stats.{name} must be float32 {list(shape)} for block_size {block_size}, "
+                             f"got {t.dtype} {tuple(t.shape)}")
+
+
 def num_selected(density: float, num_blocks: int) -> int:
     """NS = min(max(1, int(density * NT)), NT) (reference :373), via the C ABI."""
     ns = _lib.load().pasa_num_selected(float(density), int(num_blocks))
@@ -107,6 +132,7 @@ def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: i
     returned ``q_tm``, ``k_tm``, ``v_tm`` in the same pass.  ``split`` lets small grids (few
     heads x groups) spread each group over several workgroups (``pasa_block_stats_ws``;
     deterministic, the group sum in a different fixed order)."""
+    _check_qkv(q, k, v)
     _check_device(q, k, v)
     B, H, T, D = q.shape
     NT = math.ceil((T - text_tokens) / block_size)
@@ -193,6 +219,9 @@ def select_from_scores(scores: torch.Tensor, ns: int) -> Selection:
 def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_tokens: int = 0) -> torch.Tensor:
     """Phase-2 operands (kbar, V^T, Hbar^T) per (slice, group), in q's dtype (bf16 or
     fp16), as K4 stages them in LDS."""
+    if q.dim() != 4:
+        raise ValueError(f"q must be [B, H, T, D], got {tuple(q.shape)}")
+    _check_stats(stats, q, block_size, text_tokens)
     B, H, T, D = q.shape
     lib = _lib.load()
     nbytes = int(lib.pasa_sparse_attn_workspace_bytes(B * H, T, int(text_tokens), D, block_size, GROUP_SIZE))
@@ -245,12 +274,11 @@ def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: 
     the rest are padding (see ``pisa_pg_attention``).  ``placement``: q, k, v are the
     token-major view ``block_stats(..., placement)`` returned (``q_tm``, ``k_tm``,
     ``v_tm``) and the output is stored frame-major."""
+    _check_qkv(q, k, v)
     _check_device(q, k, v, pack)
     if gamma not in ("literal", "consistent"):
         raise ValueError("gamma must be 'literal' or 'consistent'")
     B, H, T, D = q.shape
-    if k.shape != q.shape or v.shape != q.shape:
-        raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     _check_selection(sel, q, block_size, text_tokens)
     o = _check_out(v, out)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), pack.data_ptr(), pack.numel(), _ptr(sel.idx),
@@ -291,12 +319,12 @@ def sparse_attn_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats
     library's static device array, so with ``out`` given the call allocates nothing
     (for code under HIP graph capture).  Shapes whose pack exceeds
     ``_lib.NOALLOC_SCRATCH_BYTES`` raise PasaError (PASA_ERR_WORKSPACE)."""
+    _check_qkv(q, k, v)
+    _check_stats(stats, q, block_size, text_tokens)
     _check_device(q, k, v, stats.kc, stats.vc, stats.hgroup)
     if gamma not in ("literal", "consistent"):
         raise ValueError("gamma must be 'literal' or 'consistent'")
     B, H, T, D = q.shape
-    if k.shape != q.shape or v.shape != q.shape:
-        raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     _check_selection(sel, q, block_size, text_tokens)
     o = _check_out(v, out)
     _lib.call("pasa_sparse_attn_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), stats.kc.data_ptr(),
@@ -315,11 +343,10 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Op
     svg/models/hyvideo/attention.py:459-476).  With ``text_tokens`` / ``text_valid``
     the attention is block-diagonal over [0, T - text_tokens + text_valid) and the
     rest (the dense HunyuanVideo path's cu_seqlens).  q, k, v: [B, H, T, 128]."""
+    _check_qkv(q, k, v)
     _check_device(q, k, v)
     B, H, T, D = q.shape
     scale = D ** -0.5 if scale is None else scale
-    if k.shape != q.shape or v.shape != q.shape:
-        raise ValueError(f"q, k, v must have one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     o = _check_out(v, out)
     tv = text_tokens if text_valid is None else text_valid
     _lib.call("pasa_dense_attn", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), float(scale), B * H, T,
