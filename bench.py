@@ -279,9 +279,14 @@ def main() -> int:
                         ("c2_block64", dataclasses.replace(wl, block_size=64)),
                         ("c3_block64", dataclasses.replace(WORKLOADS["c3"], block_size=64)),
                         ("c2_fp16", dataclasses.replace(wl, dtype=torch.float16))):
-            others[name] = config_step(torch, ops, make_inputs, w, dev, args.seed)
+            others[name] = config_step(torch, ops, make_inputs, w, dev, args.seed, permutations=(name == "c1"))
             log(f"{name}: {others[name]['ms_per_step']:.3f} ms/step, {others[name]['TFLOPs_effective']:.1f} "
                 f"TFLOP/s effective, K4 {others[name]['k4_ms']:.3f} ms")
+            if "with_permutations" in others[name]:
+                wp = others[name]["with_permutations"]
+                log(f"{name} with the layout permutations: placed {wp['placed_ms']:.3f} ms, "
+                    f"K1 + call + K1 inverse {wp['k1_separate_ms']:.3f} ms (no permutation "
+                    f"{wp['no_permutation_ms']:.3f} ms)")
 
     dit = None if args.no_dit else dit_sweep(torch, dev, args.dit_steps)
 
@@ -430,9 +435,14 @@ def power_probe(torch, ops, q, k, v, pack, sel, wl, reps: int = 4) -> dict:
                     "difference is the clock the chip holds under each (power limit), not work"}
 
 
-def config_step(torch, ops, make_inputs, wl, dev, seed: int, steps: int = 10, warmup: int = 3) -> dict:
+def config_step(torch, ops, make_inputs, wl, dev, seed: int, steps: int = 10, warmup: int = 3,
+                permutations: bool = False) -> dict:
     """ms per PISA-PG call (K2 + pack + K3 + K4, inputs resident) of another workload,
-    with its K4 time and the effective rate F / t of its algorithmic K4 FLOPs."""
+    with its K4 time and the effective rate F / t of its algorithmic K4 FLOPs.
+    ``permutations``: the workload is defined with the frame-major -> token-major layout
+    permutation of q, k, v and the inverse one of o around the call (config 1); also time
+    the call with both folded into K2/K4 (``placement=``) and K1 + call + K1 inverse,
+    five alternating calls each after a warm-up, medians."""
     q, k, v = (t.to(dev) for t in make_inputs(wl, seed=seed))
     BT, X = wl.block_size, wl.text_tokens
     ns = ops.num_selected(wl.density, wl.num_blocks())
@@ -470,6 +480,48 @@ def config_step(torch, ops, make_inputs, wl, dev, seed: int, steps: int = 10, wa
            "ms_per_step": round(ms, 4), "k4_ms": round(k4, 4), "k4_TFLOPs": round(flops / k4 / 1e9, 1),
            "k3_ms": round(k3, 4), "k2_and_pack_ms": round(k2, 4),
            "TFLOPs_effective": round(flops / ms / 1e9, 1), "flops": flops}
+    if permutations:
+        from pasa_amd import placement
+        F, Hh, W = wl.grid
+        P = Hh * W
+        pl = ops.Placement(F, P, None)
+        bufs = [torch.empty_like(t) for t in (q, k, v)]
+        o_frame = torch.empty_like(v)
+
+        def placed():
+            ops.pisa_pg_attention(q, k, v, wl.density, block_size=BT, scale=wl.op_scale, text_tokens=X,
+                                  placement=pl)
+
+        def separate():
+            placement.permute([q, k, v], bufs, F, P, X)
+            ot = ops.pisa_pg_attention(bufs[0], bufs[1], bufs[2], wl.density, block_size=BT, scale=wl.op_scale,
+                                       text_tokens=X)
+            placement.permute([ot], [o_frame], F, P, X, inverse=True)
+
+        def plain():
+            ops.pisa_pg_attention(bufs[0], bufs[1], bufs[2], wl.density, block_size=BT, scale=wl.op_scale,
+                                  text_tokens=X)
+
+        runs = {"plain": [], "placed": [], "k1_separate": []}
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        placed()
+        separate()
+        for _ in range(5):
+            for name, fn in (("plain", plain), ("placed", placed), ("k1_separate", separate)):
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                runs[name].append(e0.elapsed_time(e1))
+        pm = {name: statistics.median(v) for name, v in runs.items()}
+        res["with_permutations"] = {
+            "no_permutation_ms": round(pm["plain"], 4), "placed_ms": round(pm["placed"], 4),
+            "k1_separate_ms": round(pm["k1_separate"], 4),
+            "TFLOPs_effective_placed": round(flops / pm["placed"] / 1e9, 1),
+            "note": "frame-major q, k, v and o: the permutations folded into K2/K4 (placement=) against "
+                    "K1 forward + the call + K1 inverse, and the call on token-major inputs without any "
+                    "permutation; HIP events around one pisa_pg_attention call each, medians of five"}
+        del bufs, o_frame
     del q, k, v, out
     torch.cuda.empty_cache()
     return res
