@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 9
+#define PASA_ABI_VERSION 10
 
 typedef enum {
   PASA_OK = 0,
@@ -252,9 +252,10 @@ typedef struct {
 
 /* The placement folded into K2 and K4.  pasa_block_stats_placed reads frame-major
  * q, k, v once: it computes the statistics of their token-major view and writes that
- * view to q_tm, k_tm, v_tm (device [BH, seq_len, head_dim] in q's dtype, text rows copied in
- * place) in the same pass.  pasa_sparse_attn_packed_placed takes those token-major
- * copies as q, k, v and stores o frame-major.  Together they equal pasa_permute ->
+ * view to k_tm, v_tm and, unless it is NULL, q_tm (device [BH, seq_len, head_dim] in q's
+ * dtype, text rows copied in place) in the same pass.  pasa_sparse_attn_packed_placed takes
+ * the frame-major q itself (each query row is read once, through the placement map) and
+ * the token-major copies k_tm, v_tm as k, v, and stores o frame-major.  Together they equal pasa_permute ->
  * pasa_block_stats -> ... -> pasa_sparse_attn_packed -> inverse pasa_permute bit for
  * bit, without the permutation's separate read of q, k, v and its second pass over o.
  * head_dim 128, block_size 128; arguments otherwise as for the unplaced entry points

@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256, 1) void k2_block_stats(
 // sums are per-thread sums of its Q rows.  The Q sums and ||H_j||^2 reach LDS as per-wave
 // partials that the next block's barrier publishes (one workgroup barrier per block).
 // PERM: q, k, v are frame-major; the statistics are those of their token-major view (rm),
-// and the token-major view itself is written to qt, kt, vt: each row of a block goes out
+// and the token-major view itself is written to qt (unless NULL), kt, vt: each row of a block goes out
 // from the registers (Q) and the LDS tiles (K, V), and the workgroup of group 0 copies
 // the text rows [T, Tslice), which stay in place.
 // E: the 16-bit element type of q, k, v (Bf16 or F16).
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
         if (j * BT + r < T) {
           const int off = r * 256 + ((pc ^ (4 * (r & 3))) << 4);
           const int64_t e = slice + (int64_t)(j * BT + r) * D + pc * 8;
-          *reinterpret_cast<uint4*>(qt + e) = qv[p];
+          if (qt != nullptr) *reinterpret_cast<uint4*>(qt + e) = qv[p];
           *reinterpret_cast<uint4*>(kt + e) = lds_ld<uint4>(Kt, off);
           *reinterpret_cast<uint4*>(vt + e) = lds_ld<uint4>(Vt, off);
         }
@@ -486,7 +486,8 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     const int64_t n16 = (int64_t)(Tslice - T) * (D / 8);
     const int64_t base = slice + (int64_t)T * D;
     for (int64_t i = tid; i < n16; i += 256) {
-      *reinterpret_cast<uint4*>(qt + base + 8 * i) = *reinterpret_cast<const uint4*>(q + base + 8 * i);
+      if (qt != nullptr)
+        *reinterpret_cast<uint4*>(qt + base + 8 * i) = *reinterpret_cast<const uint4*>(q + base + 8 * i);
       *reinterpret_cast<uint4*>(kt + base + 8 * i) = *reinterpret_cast<const uint4*>(k + base + 8 * i);
       *reinterpret_cast<uint4*>(vt + base + 8 * i) = *reinterpret_cast<const uint4*>(v + base + 8 * i);
     }

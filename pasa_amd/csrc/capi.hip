@@ -248,7 +248,7 @@ int pasa_block_stats_placed(const void* q, const void* k, const void* v, void* q
                             int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
                             int64_t group_size, const pasa_placement_t* placement, int dtype, void* workspace,
                             size_t workspace_bytes, void* stream) {
-  if (!q_tm || !k_tm || !v_tm) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats_placed: NULL pointer");
+  if (!k_tm || !v_tm) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats_placed: NULL pointer");
   pasa::RowMap rm;
   int rc;
   if ((rc = check_placement(placement, bh, seq_len, text_len, head_dim, block_size, &rm))) return rc;

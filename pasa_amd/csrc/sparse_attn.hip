@@ -559,8 +559,9 @@ constexpr int kSchedDsRead = 0x100;
 
 // ALL: dense attention (every key block exact, no selection read, no correction); a
 // separate instantiation so that profiles tell the two launches apart.
-// PERM: q, k, v are the token-major view (as pasa_block_stats_placed writes it) and o
-// is stored frame-major: the store of a query row goes through map_row.
+// PERM: k and v are the token-major view (as pasa_block_stats_placed writes it), q is
+// frame-major, and o is stored frame-major: the load and the store of a query row go
+// through map_row.
 // PAIR: two consecutive query blocks (or text query tiles) per workgroup (not ALL,
 // not PERM).  Video blocks visit NS selected tiles each, so their barriers match
 // (a shorter selection row, or a text pair spanning the prompt and the padding
@@ -650,10 +651,13 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   const uint32_t slice_bytes = (uint32_t)Ttot * D * 2u;
   const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
 
+  // PERM: q is frame-major (only k and v are token-major copies); each lane gathers its
+  // own query row through the same map as its output store.
+  const int qrow_ld = perm ? qrow_st : qrow;
   typename E::vec8 qf[D / 16];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks)
-    qf[ks] = as_vec8<E>(buf_load16(qr, ((uint32_t)qrow * D + ks * 16 + h * 8) * 2u));
+    qf[ks] = as_vec8<E>(buf_load16(qr, ((uint32_t)qrow_ld * D + ks * 16 + h * 8) * 2u));
   // Complete the Q loads now: vector-memory waits the compiler would place at their
   // first use inside the loop would also wait for the tile loads in flight there.
   wait_vmcnt<0>();

@@ -83,8 +83,9 @@ def num_selected(density: float, num_blocks: int) -> int:
 @dataclass
 class BlockStats:
     """Outputs of K2.  Statistics fp32: qc/kc/vc [B,H,NT,D], hnorm [B,H,NT], hgroup
-    [B,H,NG,D,D].  With a placement, also the token-major view of q, k, v (in q's dtype),
-    which the placed attention call reads."""
+    [B,H,NG,D,D].  With a placement, also the token-major view of k and v (in q's dtype),
+    which the placed attention call reads; q_tm stays None (that call gathers q's rows
+    frame-major)."""
     qc: torch.Tensor
     kc: torch.Tensor
     vc: torch.Tensor
@@ -128,8 +129,9 @@ def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: i
     Replaces fused_chunk_reduce (reference :268-288; hc is never materialised)
     followed by compute_h_group (:291-301).  With ``text_tokens`` the blocks cover
     the first T - text_tokens rows only.  With ``placement`` the statistics are those
-    of the token-major view of frame-major q, k, v, and that view is written to the
-    returned ``q_tm``, ``k_tm``, ``v_tm`` in the same pass.  ``split`` lets small grids (few
+    of the token-major view of frame-major q, k, v, and the view of k and v is written to
+    the returned ``k_tm``, ``v_tm`` in the same pass (the attention call reads q frame-major
+    through the placement map, so ``q_tm`` is None).  ``split`` lets small grids (few
     heads x groups) spread each group over several workgroups (``pasa_block_stats_ws``;
     deterministic, the group sum in a different fixed order)."""
     _check_qkv(q, k, v)
@@ -155,11 +157,11 @@ def block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: i
         _lib.call("pasa_block_stats", *args, _DTYPES.get(q.dtype, -1), _stream(q))
     else:
         st, _keep = placement.struct(q.device, B, H)
-        q_tm, k_tm, v_tm = (torch.empty_like(t) for t in (q, k, v))
-        _lib.call("pasa_block_stats_placed", q.data_ptr(), k.data_ptr(), v.data_ptr(), q_tm.data_ptr(),
+        k_tm, v_tm = torch.empty_like(k), torch.empty_like(v)
+        _lib.call("pasa_block_stats_placed", q.data_ptr(), k.data_ptr(), v.data_ptr(), None,
                   k_tm.data_ptr(), v_tm.data_ptr(), *args[3:], ctypes.byref(st), _DTYPES.get(q.dtype, -1),
                   ws_ptr, ws_bytes, _stream(q))
-        return BlockStats(qc, kc, vc, hnorm, hgroup, q_tm, k_tm, v_tm)
+        return BlockStats(qc, kc, vc, hnorm, hgroup, None, k_tm, v_tm)
     return BlockStats(qc, kc, vc, hnorm, hgroup)
 
 
@@ -271,9 +273,9 @@ def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: 
                        text_valid: Optional[int] = None, placement: Optional[Placement] = None) -> torch.Tensor:
     """K4 on operands from ``pack_phase2``.  ``text_valid`` (default: all
     ``text_tokens``) is the number of prompt rows at the start of the text segment;
-    the rest are padding (see ``pisa_pg_attention``).  ``placement``: q, k, v are the
-    token-major view ``block_stats(..., placement)`` returned (``q_tm``, ``k_tm``,
-    ``v_tm``) and the output is stored frame-major."""
+    the rest are padding (see ``pisa_pg_attention``).  ``placement``: q is frame-major
+    (the tensor given to ``block_stats(..., placement)``), k and v are the token-major
+    view that call returned (``k_tm``, ``v_tm``), and the output is stored frame-major."""
     _check_qkv(q, k, v)
     _check_device(q, k, v, pack)
     if gamma not in ("literal", "consistent"):
@@ -301,12 +303,13 @@ def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockS
     correction of the rest (reference pisa_pg_fwd_kernel :135-262); with
     ``text_tokens``, the prompt keys are exact for every video query block and the
     text rows are dense within their segment.  With ``placement`` (q, k, v frame-major)
-    the call reads the token-major view ``stats`` holds and stores o frame-major."""
+    the call reads q's rows through the placement map and k, v from the token-major view
+    ``stats`` holds, and stores o frame-major."""
     pack = pack_phase2(q, stats, block_size, text_tokens)
-    if placement is not None:  # the token-major view K2 wrote; the output goes back frame-major
-        if stats.q_tm is None:
+    if placement is not None:  # the token-major k, v K2 wrote; the output goes back frame-major
+        if stats.k_tm is None or stats.v_tm is None:
             raise ValueError("placement needs the statistics of block_stats(..., placement=...)")
-        q, k, v = stats.q_tm, stats.k_tm, stats.v_tm
+        k, v = stats.k_tm, stats.v_tm
     return sparse_attn_packed(q, k, v, pack, sel, scale, block_size, gamma, out, text_tokens, text_valid,
                               placement)
 
