@@ -45,6 +45,26 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem, bool f32, 
   }
 }
 
+// 16-byte row chunks, streamed (nontemporal: not kept in L2 or the last-level cache) when
+// NT, for rows of tensors too large for those caches to help their next reader.
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void* ptr) {
+  if constexpr (NT) {
+    const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr));
+    return uint4{t[0], t[1], t[2], t[3]};
+  } else {
+    return *reinterpret_cast<const uint4*>(ptr);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void st16(void* ptr, const uint4& v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store((u32x4_t){v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(ptr));
+  else
+    *reinterpret_cast<uint4*>(ptr) = v;
+}
+
+template <bool NT = false>
 __device__ __forceinline__ void store8(void* base, int64_t elem, bool f32, const float (&f)[8]) {
   if (f32) {
     float4* p = reinterpret_cast<float4*>(reinterpret_cast<float*>(base) + elem);
@@ -56,7 +76,7 @@ __device__ __forceinline__ void store8(void* base, int64_t elem, bool f32, const
     o.y = pack_bf16x2(f[2], f[3]);
     o.z = pack_bf16x2(f[4], f[5]);
     o.w = pack_bf16x2(f[6], f[7]);
-    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(base) + elem) = o;
+    st16<NT>(reinterpret_cast<uint16_t*>(base) + elem, o);
   }
 }
 
@@ -93,7 +113,8 @@ struct RowStore<CPT, false> {
   }
 };
 
-template <int CPT, bool PACKED>
+// NT (packed rows only): the row tensors x, the residual, h and y are streamed.
+template <int CPT, bool PACKED, bool NT>
 __global__ __launch_bounds__(256) void k6_row_ops(RowOpParams p) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -113,7 +134,7 @@ __global__ __launch_bounds__(256) void k6_row_ops(RowOpParams p) {
         st.zero(i);
       } else if constexpr (PACKED) {
         reinterpret_cast<uint4*>(&st)[i] =
-            *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.x) + base + 8 * (lane + 64 * i));
+            ld16<NT>(reinterpret_cast<const uint16_t*>(p.x) + base + 8 * (lane + 64 * i));
       } else {
         float f[8];
         load8(p.x, base + 8 * (lane + 64 * i), p.x_f32, f);
@@ -127,8 +148,8 @@ __global__ __launch_bounds__(256) void k6_row_ops(RowOpParams p) {
     for (int i = 0; i < CPT; ++i) {
       if (i >= nmine) continue;
       const int c0 = 8 * (lane + 64 * i);
-      xr[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.x) + base + c0);
-      rr[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.r) + base + c0);
+      xr[i] = ld16<NT>(reinterpret_cast<const uint16_t*>(p.x) + base + c0);
+      rr[i] = ld16<NT>(reinterpret_cast<const uint16_t*>(p.r) + base + c0);
     }
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -151,7 +172,7 @@ __global__ __launch_bounds__(256) void k6_row_ops(RowOpParams p) {
       }
       st.set(i, h);  // h rounded to bf16, its storage type
       if (p.h != nullptr)
-        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.h) + base + c0) = reinterpret_cast<uint4*>(&st)[i];
+        st16<NT>(reinterpret_cast<uint16_t*>(p.h) + base + c0, reinterpret_cast<uint4*>(&st)[i]);
     }
   } else {
     // ---- stage A, other types ---------------------------------------------------------
@@ -246,13 +267,14 @@ __global__ __launch_bounds__(256) void k6_row_ops(RowOpParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = add_rn(mul_rn(v[e], add_rn(1.0f, sc[e])), sh[e]);
     }
-    store8(p.y, base + c0, p.y_f32, v);
+    store8<NT>(p.y, base + c0, p.y_f32, v);
   }
 }
 
 }  // namespace
 
 constexpr int kRowOpsMaxCpt = 16;  // N <= 8192
+constexpr int64_t kStreamBytes = int64_t(256) << 20;  // MI355X last-level (Infinity) cache
 int row_ops_max_cols() { return kRowOpsMaxCpt * 64 * 8; }
 
 hipError_t launch_row_ops(const RowOpParams& p, hipStream_t stream) {
@@ -265,10 +287,15 @@ hipError_t launch_row_ops(const RowOpParams& p, hipStream_t stream) {
   // Packed: stage B's input is bf16 and, with stage A, x and the residual are bf16 too
   // (every call of the Wan block).  Other type mixes keep the row in fp32 registers.
   const bool packed = p.r != nullptr ? (!p.h_f32 && !p.x_f32 && !p.r_f32) : !p.x_f32;
-#define PASA_K6(C)                                                                        \
-  do {                                                                                    \
-    if (packed) hipLaunchKernelGGL((k6_row_ops<C, true>), grid, dim3(256), 0, stream, p);  \
-    else hipLaunchKernelGGL((k6_row_ops<C, false>), grid, dim3(256), 0, stream, p);        \
+  // Rows of a tensor larger than the 256 MB last-level cache are streamed: its next reader
+  // cannot find them there anyway, and nontemporal accesses move them 15% faster (75,600 x
+  // 5120 bf16: 0.58 against 0.68 ms).  Smaller tensors stay cached for their reader.
+  const bool stream_rows = packed && (int64_t)p.M * p.N * 2 >= kStreamBytes;
+#define PASA_K6(C)                                                                              \
+  do {                                                                                          \
+    if (stream_rows) hipLaunchKernelGGL((k6_row_ops<C, true, true>), grid, dim3(256), 0, stream, p); \
+    else if (packed) hipLaunchKernelGGL((k6_row_ops<C, true, false>), grid, dim3(256), 0, stream, p); \
+    else hipLaunchKernelGGL((k6_row_ops<C, false, false>), grid, dim3(256), 0, stream, p);     \
   } while (0)
   if (cpt <= 1) PASA_K6(1);
   else if (cpt <= 2) PASA_K6(2);

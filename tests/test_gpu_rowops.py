@@ -115,3 +115,30 @@ def test_c4_rows(device):
     y = MOD.ln_modulate(x.to(device), sc.to(device), sh.to(device), 1e-6)
     torch.cuda.synchronize()
     same(y, R.row_ops(x, layernorm=True, scale=sc, shift=sh)[1], "c4 rows")
+
+
+def test_streamed_rows_equal_cached_rows(device):
+    """Row tensors of 256 MB or more take the streamed (nontemporal) kernel; rows are
+    independent, so one call over 16,400 x 8192 bf16 rows (269 MB) must equal the same
+    rows in two calls of 8,200 (134 MB each, the cached kernel) bit for bit: the gated
+    residual in place plus LayerNorm affine, the heaviest call of the block."""
+    M, N = 16400, 8192
+    g = torch.Generator(device=device).manual_seed(7)
+    x = torch.randn(1, M, N, device=device, dtype=torch.bfloat16, generator=g)
+    h0 = torch.randn(1, M, N, device=device, dtype=torch.bfloat16, generator=g)
+    gate = torch.randn(1, 1, N, device=device, generator=g)
+    w = torch.randn(N, device=device, dtype=torch.bfloat16, generator=g)
+    b = torch.randn(N, device=device, dtype=torch.bfloat16, generator=g)
+    h_one, y_one = h0.clone(), torch.empty_like(h0)
+    MOD.row_ops(x, residual=h_one, gate=gate, h_out=h_one, layernorm=True, weight=w, bias=b, y=y_one, eps=1e-6)
+    h_two, y_two = h0.clone(), torch.empty_like(h0)
+    for r0 in (0, M // 2):
+        sl = slice(r0, r0 + M // 2)
+        hs, ys = h_two[:, sl].contiguous(), torch.empty(1, M // 2, N, device=device, dtype=torch.bfloat16)
+        MOD.row_ops(x[:, sl].contiguous(), residual=hs, gate=gate, h_out=hs, layernorm=True, weight=w, bias=b,
+                    y=ys, eps=1e-6)
+        h_two[:, sl] = hs
+        y_two[:, sl] = ys
+    torch.cuda.synchronize()
+    same(h_one, h_two.cpu(), "streamed vs cached gated residual")
+    same(y_one, y_two.cpu(), "streamed vs cached LayerNorm")
