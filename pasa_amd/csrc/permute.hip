@@ -5,13 +5,14 @@
 // reference walks source rows and scatters; here each thread owns one 16-byte
 // chunk of a DESTINATION row and gathers it, so every wavefront writes whole,
 // contiguous destination rows (coalesced stores) and reads whole source rows.
-// Up to three tensors share one launch (the index math is computed once).
+// Up to three tensors share one launch, one tensor per workgroup (blockIdx.z): a
+// wavefront that moved the same chunk of all three at once ran at 5.6 TB/s, one tensor
+// at a time at 6.2 TB/s (c2 forward, [40, 75600, 128] bf16 x 3).
 #include "common.h"
 #include "kernels.h"
 
 namespace pasa {
 
-template <int NTENS>
 __global__ __launch_bounds__(256) void k1_permute(
     const u32x4_t* __restrict__ s0, const u32x4_t* __restrict__ s1,
     const u32x4_t* __restrict__ s2, u32x4_t* __restrict__ d0, u32x4_t* __restrict__ d1,
@@ -19,6 +20,9 @@ __global__ __launch_bounds__(256) void k1_permute(
     int S, int F, int P, int ctx, int chunks_per_row, int rows_per_wg,
     const int32_t* __restrict__ head_is_temporal, int inverse) {
   const int bh = blockIdx.y;
+  const int t = blockIdx.z;  // which tensor
+  const u32x4_t* __restrict__ src_t = t == 0 ? s0 : (t == 1 ? s1 : s2);
+  u32x4_t* __restrict__ dst_t = t == 0 ? d0 : (t == 1 ? d1 : d2);
   const int local_row = threadIdx.x / chunks_per_row;
   const int chunk = threadIdx.x - local_row * chunks_per_row;
   const int r = blockIdx.x * rows_per_wg + local_row;
@@ -40,13 +44,7 @@ __global__ __launch_bounds__(256) void k1_permute(
   const int64_t base = (int64_t)bh * S * chunks_per_row;
   const int64_t so = base + (int64_t)src * chunks_per_row + chunk;
   const int64_t dof = base + (int64_t)r * chunks_per_row + chunk;
-  u32x4_t a = __builtin_nontemporal_load(s0 + so);
-  u32x4_t b, c;
-  if (NTENS > 1) b = __builtin_nontemporal_load(s1 + so);
-  if (NTENS > 2) c = __builtin_nontemporal_load(s2 + so);
-  __builtin_nontemporal_store(a, d0 + dof);
-  if (NTENS > 1) __builtin_nontemporal_store(b, d1 + dof);
-  if (NTENS > 2) __builtin_nontemporal_store(c, d2 + dof);
+  __builtin_nontemporal_store(__builtin_nontemporal_load(src_t + so), dst_t + dof);
 }
 
 hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* d0, void* d1,
@@ -57,22 +55,11 @@ hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* 
   const int threads = 256;
   const int rows_per_wg = cpr >= threads ? 1 : threads / cpr;
   if (cpr > threads) return hipErrorInvalidValue;  // rejected by the host validation
-  dim3 grid((S + rows_per_wg - 1) / rows_per_wg, bh);
-  auto a0 = (const u32x4_t*)s0;
-  auto a1 = (const u32x4_t*)s1;
-  auto a2 = (const u32x4_t*)s2;
-  auto b0 = (u32x4_t*)d0;
-  auto b1 = (u32x4_t*)d1;
-  auto b2 = (u32x4_t*)d2;
-  if (ntens == 1)
-    hipLaunchKernelGGL(k1_permute<1>, grid, dim3(threads), 0, stream, a0, a1, a2, b0, b1, b2, S, F,
-                       P, ctx, cpr, rows_per_wg, head_is_temporal, inverse);
-  else if (ntens == 2)
-    hipLaunchKernelGGL(k1_permute<2>, grid, dim3(threads), 0, stream, a0, a1, a2, b0, b1, b2, S, F,
-                       P, ctx, cpr, rows_per_wg, head_is_temporal, inverse);
-  else
-    hipLaunchKernelGGL(k1_permute<3>, grid, dim3(threads), 0, stream, a0, a1, a2, b0, b1, b2, S, F,
-                       P, ctx, cpr, rows_per_wg, head_is_temporal, inverse);
+  if (ntens < 1 || ntens > 3) return hipErrorInvalidValue;
+  dim3 grid((S + rows_per_wg - 1) / rows_per_wg, bh, ntens);
+  hipLaunchKernelGGL(k1_permute, grid, dim3(threads), 0, stream, (const u32x4_t*)s0, (const u32x4_t*)s1,
+                     (const u32x4_t*)s2, (u32x4_t*)d0, (u32x4_t*)d1, (u32x4_t*)d2, S, F, P, ctx, cpr,
+                     rows_per_wg, head_is_temporal, inverse);
   return hipGetLastError();
 }
 
