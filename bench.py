@@ -48,6 +48,8 @@ def main() -> int:
     ap.add_argument("--dit-steps", type=int, default=2, help="timed denoising steps per c4 variant")
     ap.add_argument("--power-probe", action="store_true",
                     help="run only the K4 power probe (real vs all-zero operands) and print its JSON")
+    ap.add_argument("--no-power-probe", action="store_true",
+                    help="skip the power probe's K4 launches (profiles that average K4 over dispatches)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -127,9 +129,11 @@ def main() -> int:
     log(f"ms/step {ms_per_step:.3f}  K2 {k2_only:.3f} + pack {pack_ms:.3f}  K3 {k3:.3f}  K4 {k4:.3f} ms  "
         f"-> {value:.1f} TFLOP/s effective, K4 {achieved:.1f} TFLOP/s")
 
-    probe = power_probe(torch, ops, q, k, v, ops.pack_phase2(q, last_sel[1], BT, X), last_sel[0], wl)
-    log(f"K4 power probe: real operands {probe['k4_real_ms']:.3f} ms, all-zero operands "
-        f"{probe['k4_zero_operands_ms']:.3f} ms (x{probe['real_over_zero']:.3f})")
+    probe = None
+    if not args.no_power_probe:
+        probe = power_probe(torch, ops, q, k, v, ops.pack_phase2(q, last_sel[1], BT, X), last_sel[0], wl)
+        log(f"K4 power probe: real operands {probe['k4_real_ms']:.3f} ms, all-zero operands "
+            f"{probe['k4_zero_operands_ms']:.3f} ms (x{probe['real_over_zero']:.3f})")
 
     # K1: frame-major <-> token-major permutation of Q, K, V (forward) and O (inverse).
     F, Hh, W = wl.grid
