@@ -357,6 +357,17 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Op
     return o
 
 
+def kernel_head_dim(head_dim: int, dtype: torch.dtype, text_tokens: int = 0, placed: bool = False) -> int:
+    """The head dim the gfx950 kernels run a call of ``head_dim`` at: 64 (bf16, no text
+    segment, no placement) or 128.  ``pisa_pg_attention`` zero-pads smaller head dims to it,
+    as the reference pads to BK = min(128, next_pow2(D)) (:346-347)."""
+    if head_dim < 1 or head_dim > 128:
+        raise ValueError(f"head_dim must be in [1, 128] (the reference's BK = min(128, next_pow2(D))), got {head_dim}")
+    if head_dim <= 64 and dtype == torch.bfloat16 and not text_tokens and not placed:
+        return 64
+    return 128
+
+
 def pisa_pg_attention(
     q, k, v,
     density=0.15,
@@ -377,7 +388,7 @@ def pisa_pg_attention(
 ):
     """PISA with per-group first-order correction (drop-in for reference :307-398).
 
-    q, k, v: [B, H, T, D] contiguous bf16 (or fp16 at D = 128) on a ROCm device; returns o like v.
+    q, k, v: [B, H, T, D] contiguous bf16 or fp16, D <= 128, on a ROCm device; returns o like v.
     ``timestep``, ``verbose`` and ``prompt_token_length`` do not change the math
     (as in the reference, where ``prompt_token_length`` is documented but unused).
     ``use_random`` adds one N(0,1) draw per key block to the selection score; pass
@@ -398,11 +409,23 @@ def pisa_pg_attention(
     ``placement``: q, k, v are frame-major (HunyuanVideo's layout) and the operator
     runs on their token-major view, returning o frame-major; equal to the
     reference's hunyuan_sparse_head_placement -> attention -> hunyuan_hidden_states_placement
-    (svg/models/hyvideo/attention.py:412-446) in one pass (D = 128, block_size 128)."""
+    (svg/models/hyvideo/attention.py:412-446) in one pass (block_size 128).
+    Head dims other than 64 and 128 (and 64 where the call needs the 128 kernels: fp16, a
+    text segment, a placement) run zero-padded to ``kernel_head_dim``: zero features add
+    nothing to a score, a block mean or the first-order moment, so the result is the
+    unpadded math; the padded output features are dropped."""
+    _check_qkv(q, k, v)
     B, H, T, D = q.shape
     if group_size != GROUP_SIZE:
         raise ValueError(f"the gfx950 kernels use group_size={GROUP_SIZE}")
     scale = D ** -0.5 if scale is None else scale
+    Dk = kernel_head_dim(D, q.dtype, text_tokens, placement is not None)
+    if Dk != D:
+        pad = lambda t: torch.nn.functional.pad(t, (0, Dk - D)).contiguous()
+        o = pisa_pg_attention(pad(q), pad(k), pad(v), density, timestep, block_size, group_size, scale,
+                              use_cov_bias, use_random, verbose, prompt_token_length, noise=noise, gamma=gamma,
+                              text_tokens=text_tokens, text_valid=text_valid, placement=placement)
+        return o[..., :D].contiguous()
     NT = math.ceil((T - text_tokens) / block_size)
     stats = block_stats(q, k, v, block_size, group_size, text_tokens, placement)
     if use_random and use_cov_bias and noise is None:

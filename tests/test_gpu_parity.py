@@ -733,3 +733,39 @@ def test_placed_attention_equals_permute_attend_unpermute(device, F, P, text, fl
     PL.hunyuan_hidden_states_placement(ot, ref, mask, text, F, P)
     torch.cuda.synchronize()
     assert torch.equal(o, ref)
+
+
+HEAD_DIM_CASES = [  # (head dim, dtype, text tokens, block size)
+    (96, torch.bfloat16, 0, 64),
+    (32, torch.bfloat16, 0, 64),
+    (80, torch.bfloat16, 0, 128),
+    (64, torch.float16, 0, 64),
+    (64, torch.bfloat16, 128, 64),
+    (48, torch.float16, 64, 128),
+]
+
+
+@pytest.mark.parametrize("D,dtype,text,BT", HEAD_DIM_CASES)
+def test_operator_pads_other_head_dims(device, D, dtype, text, BT):
+    """pisa_pg_attention at a head dim the kernels do not take directly (or 64 where the
+    call needs the D = 128 kernels: fp16, a text segment) runs zero-padded and returns
+    the unpadded math: compared with the oracle at the true head dim, on the selection
+    the kernels make for the padded inputs, to the reference-precision floor."""
+    wl = Workload("hd", heads=2, head_dim=D, grid=(4, 16, 24), block_size=BT, density=0.2, text_tokens=text,
+                  prescale=D ** -0.5 / 128 ** -0.5, dtype=dtype)
+    q, k, v = make_inputs(wl, seed=11, dtype=dtype)
+    say(f"[head dim] D={D} {dtype} text={text} BT={BT} T={wl.seq_len}")
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    scale = D ** -0.5
+    o = ops.pisa_pg_attention(qd, kd, vd, wl.density, block_size=BT, scale=scale, text_tokens=text)
+    assert o.shape == q.shape and o.dtype == dtype
+    Dk = ops.kernel_head_dim(D, dtype, text)
+    assert Dk != D or D == 64
+    pad = lambda t: torch.nn.functional.pad(t, (0, Dk - D)).contiguous()
+    st = ops.block_stats(pad(qd), pad(kd), pad(vd), BT, 32, text_tokens=text)
+    sel = ops.select_blocks(st, wl.density, scale)
+    kw = dict(indices=sel.idx.cpu(), text_tokens=text)
+    ref = O.pisa_pg_attention(q, k, v, wl.density, BT, 32, scale, **kw)
+    rp = O.pisa_pg_attention(q, k, v, wl.density, BT, 32, scale, ref_precision=dtype, **kw)
+    check_parity(o.cpu(), ref, f"head dim {D} {dtype} text {text} BT{BT}", O.parity_metrics(rp, ref, dtype), dtype)
+

@@ -52,3 +52,18 @@ def test_pack_rejects_statistics_of_another_block_size():
     bad.kc = bad.kc.double()
     with pytest.raises(ValueError, match="float32"):
         ops.pack_phase2(q, bad, 64)
+
+
+def test_kernel_head_dim():
+    """The head dim a call runs at: 64 for bf16 without a text segment or placement, else
+    128 (the reference's BK = min(128, next_pow2(D)) padding, at the two widths the kernels
+    take); above 128 is an error."""
+    bf, f16 = torch.bfloat16, torch.float16
+    assert [ops.kernel_head_dim(d, bf) for d in (1, 32, 63, 64)] == [64] * 4
+    assert [ops.kernel_head_dim(d, bf) for d in (65, 80, 96, 128)] == [128] * 4
+    assert ops.kernel_head_dim(64, f16) == 128
+    assert ops.kernel_head_dim(32, bf, text_tokens=256) == 128
+    assert ops.kernel_head_dim(64, bf, placed=True) == 128
+    for d in (0, 129, 256):
+        with pytest.raises(ValueError, match="head_dim"):
+            ops.kernel_head_dim(d, bf)
