@@ -218,10 +218,12 @@ int pasa_sparse_attn_packed(const void* q, const void* k, const void* v, const v
  * a static device array of PASA_NOALLOC_SCRATCH_BYTES bytes that the library holds on
  * every GPU it runs on until the process ends, so the call allocates nothing and
  * needs no caller buffer beyond its inputs and outputs.  Its size limits the shape:
- * bh * ceil(ceil((seq_len - text_len) / block_size) / 32) * 53,248 bytes must fit
- * (1,260 slice-groups: the Wan2.1-14B 720p shape at block size 128, 760; HunyuanVideo
- * 720p at block size 128, 720; Wan2.1-1.3B at block size 64, 192); a larger shape
- * returns PASA_ERR_WORKSPACE before any launch.  Calls on one GPU share its array,
+ * pasa_sparse_attn_workspace_bytes(...) <= PASA_NOALLOC_SCRATCH_BYTES must hold.  That
+ * is bh * ceil(ceil((seq_len - text_len) / block_size) / 32) slice-groups of 53,248 bytes
+ * each at head_dim 128 (1,260 slice-groups fit: the Wan2.1-14B 720p shape at block size
+ * 128 needs 760, HunyuanVideo 720p at block size 128 720, Wan2.1-1.3B at block size 64
+ * 192) and of 20,480 bytes each at head_dim 64 (3,276 fit); a larger shape returns
+ * PASA_ERR_WORKSPACE before any launch.  Calls on one GPU share its array,
  * so calls that overlap on one GPU race; calls in stream order do not.  The first
  * call on a device looks the array's address up (hipGetSymbolAddress) and caches it.
  * Arguments and results otherwise as pasa_sparse_attn (same kernels, bitwise-equal
@@ -258,6 +260,8 @@ typedef struct {
  * the token-major copies k_tm, v_tm as k, v, and stores o frame-major.  Together they equal pasa_permute ->
  * pasa_block_stats -> ... -> pasa_sparse_attn_packed -> inverse pasa_permute bit for
  * bit, without the permutation's separate read of q, k, v and its second pass over o.
+ * The copies are written while q, k, v are read: a copy that overlaps q, k, v or another
+ * copy (an in-place permutation) returns PASA_ERR_BAD_ARG.
  * head_dim 128, block_size 128; arguments otherwise as for the unplaced entry points
  * (pasa_block_stats_placed's workspace as pasa_block_stats_ws's: with the same
  * workspace the group moments equal the unplaced call's bit for bit).

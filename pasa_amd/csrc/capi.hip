@@ -253,6 +253,25 @@ int pasa_block_stats_placed(const void* q, const void* k, const void* v, void* q
   int rc;
   if ((rc = check_placement(placement, bh, seq_len, text_len, head_dim, block_size, &rm))) return rc;
   void* const copies[3] = {q_tm, k_tm, v_tm};
+  // The copies are written while q, k, v are still being read (and each other's rows are
+  // distinct), so none may overlap an input or another copy.
+  if (bh > 0 && seq_len > 0 && bh <= kMaxGridY && seq_len <= kMaxI32 / 2) {
+    const uintptr_t bytes = (uintptr_t)(bh * seq_len * head_dim * 2);
+    const void* const inputs[3] = {q, k, v};
+    const char* const names[3] = {"q", "k", "v"};
+    for (int i = 0; i < 3; ++i) {
+      if (!copies[i]) continue;
+      const uintptr_t a = (uintptr_t)copies[i];
+      for (int j = 0; j < 3; ++j) {
+        const uintptr_t b = (uintptr_t)inputs[j];
+        if (b && a < b + bytes && b < a + bytes)
+          return fail(PASA_ERR_BAD_ARG, "pasa_block_stats_placed: %s_tm overlaps %s", names[i], names[j]);
+        const uintptr_t c = (uintptr_t)copies[j];
+        if (j != i && c && a < c + bytes && c < a + bytes)
+          return fail(PASA_ERR_BAD_ARG, "pasa_block_stats_placed: %s_tm overlaps %s_tm", names[i], names[j]);
+      }
+    }
+  }
   return block_stats_impl(q, k, v, qc, kc, vc, hnorm, hgroup, bh, seq_len, text_len, head_dim, block_size,
                           group_size, dtype, &rm, copies, workspace, workspace_bytes, stream);
 }

@@ -327,6 +327,23 @@ H16 = 3 << 40
 Y16 = 4 << 40
 
 
+@pytest.mark.parametrize("q_tm,k_tm,v_tm", [
+    (None, G16, Y16),              # k_tm is k (an in-place permutation)
+    (None, Y16, H16 + 4096),       # v_tm starts inside v
+    (F16, Y16, Y16 + (1 << 36)),   # q_tm is q
+    (None, Y16, Y16 + 4096),       # the two copies overlap
+])
+def test_placed_copies_must_not_overlap(lib, q_tm, k_tm, v_tm):
+    """pasa_block_stats_placed writes the token-major copies while it reads q, k, v: a copy
+    that overlaps an input or another copy is rejected before any launch."""
+    import ctypes
+    from pasa_amd._lib import Placement
+    pl = Placement(8, 120, None, 2)
+    rc = lib.pasa_block_stats_placed(F16, G16, H16, q_tm, k_tm, v_tm, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1000, 40,
+                                     128, 128, 32, ctypes.byref(pl), 0, None, 0, None)
+    assert rc == -9 and b"overlaps" in lib.pasa_last_error()
+
+
 def row_ops(lib, **kw):
     a = dict(x=F16, xdt=0, r=G16, rdt=0, gate=F16 + (1 << 36), h=G16, hdt=0, ln=1, w=None, b=None, wbdt=0,
              scale=F16 + (2 << 36), shift=F16 + (3 << 36), y=Y16, ydt=0, M=64, N=1536, S=64, ps=0, eps=1e-6)

@@ -17,6 +17,7 @@ evaluation of the same bf16 inputs:
 End to end, GPU and CPU fp32 scores differ in the last ulp, so a query block may
 pick a different block at an exact or near tie; the test proves every such
 difference is a near tie and checks the other query blocks elementwise."""
+import dataclasses
 import math
 import os
 import sys
@@ -483,17 +484,70 @@ def test_end_to_end_c3_full_shape_two_heads(device):
     assert r["kernel_over_floor"] <= 1.5
 
 
-@pytest.mark.parametrize("name,text_valid", [("c2", None), ("c3", 141)])
-def test_end_to_end_block64_one_head(device, name, text_valid):
-    """Block size 64, the processors' default: query blocks run in pairs.  At the c3 layout
-    141 of the 256 text rows are the prompt (three prompt tiles, an odd count, so one pair
-    holds the last prompt tile and the first padding tile)."""
-    wl = small_workload(WORKLOADS[name], heads=1, grid=WORKLOADS[name].grid, block_size=64)
-    say(f"[E2E] {name} shape at block 64, 1 head: {wl.video_tokens} video + {wl.text_tokens} text tokens "
+@pytest.mark.parametrize("name,text_valid", [("c2", None), ("c3", None), ("c3", 141)])
+def test_end_to_end_block64_first_and_last_head(device, name, text_valid):
+    """Block size 64, the processors' default (query blocks run in pairs), at the full c2 and
+    c3 shapes as bench.py times them (``c2_block64``, ``c3_block64``): the first and the last
+    head.  With text_valid 141 of the 256 text rows are the prompt (three prompt tiles, an
+    odd count, so one pair holds the last prompt tile and the first padding tile)."""
+    wl = dataclasses.replace(WORKLOADS[name], block_size=64)
+    heads = (0, wl.heads - 1)
+    say(f"[E2E] {name} shape at block 64, heads {heads}: {wl.video_tokens} video + {wl.text_tokens} text tokens "
         f"(valid {text_valid}), NT {wl.num_blocks()}")
-    q, k, v, o, st, idx = run_heads(wl, range(0, 1), device, text_valid)
-    r = check_end_to_end(o, q, k, v, wl, st, idx, (0,), None, f"{name} block 64", text_valid=text_valid)
+    q, k, v, o, st, idx = run_heads(wl, heads, device, text_valid)
+    r = check_end_to_end(o, q, k, v, wl, st, idx, (0, 1), None, f"{name} block 64", text_valid=text_valid)
+    say(f"[E2E] {name} block 64: kernel/floor max-abs ratio {r['kernel_over_floor']:.3f}")
     assert r["kernel_over_floor"] <= 1.5
+
+
+def test_end_to_end_c2_fp16_one_head(device):
+    """fp16 q, k, v end to end at the c2 shape (bench.py's ``c2_fp16``), head 0: the GPU
+    selection is the exact top-k up to near ties, and the output meets the bound against
+    the fp32 oracle on that selection, within 1.5x (+ one fp16 ulp) of the oracle run at
+    the reference's roundings in fp16."""
+    wl = dataclasses.replace(WORKLOADS["c2"], dtype=torch.float16)
+    say(f"[E2E] c2 fp16, head 0: T={wl.seq_len}, NT {wl.num_blocks()}")
+    q, k, v = make_inputs(wl, seed=0, heads=range(0, 1))
+    assert q.dtype == torch.float16
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    o = ops.pisa_pg_attention(qd, kd, vd, density=wl.density, block_size=wl.block_size, scale=wl.op_scale)
+    assert o.dtype == torch.float16
+    st = ops.block_stats(qd, kd, vd, wl.block_size, 32)
+    sel = ops.select_blocks(st, wl.density, wl.op_scale)
+    idx = sel.idx.cpu()
+    check_selection_near_ties(st, idx, wl.op_scale, sel.ns, (0,), None, "c2 fp16")
+    ref = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, indices=idx)
+    rp = O.pisa_pg_attention(q, k, v, wl.density, wl.block_size, 32, wl.op_scale, indices=idx,
+                             ref_precision=torch.float16)
+    floor = O.parity_metrics(rp, ref, torch.float16)
+    m = check_parity(o.cpu(), ref, "c2 fp16 head 0 (GPU selection)", floor, torch.float16)
+    ratio = m["max_abs"] / floor["max_abs"]
+    say(f"[E2E] c2 fp16 head 0: kernel/floor max-abs ratio {ratio:.3f}")
+    assert ratio <= 1.5
+
+
+@pytest.mark.parametrize("name,heads", [("c1", None), ("c2", (0, 39))])
+def test_placed_route_at_bench_shapes(device, name, heads):
+    """The placed call (placement folded into K2/K4) is bit-identical to K1 -> call -> K1
+    inverse at the shapes bench.py times both routes: all 12 heads of c1 (F 21, P 1560,
+    ``other_configs.c1.with_permutations``) and the first and last head of c2 (F 21,
+    P 3600, ``placement_folded``)."""
+    wl = WORKLOADS[name]
+    hs = range(wl.heads) if heads is None else heads
+    F, Hh, W = wl.grid
+    P, X = Hh * W, wl.text_tokens
+    say(f"[placed] {name}: heads {list(hs)}, F={F} P={P}")
+    q, k, v = make_inputs(wl, seed=0, heads=hs, device=device)
+    o = ops.pisa_pg_attention(q, k, v, wl.density, block_size=wl.block_size, scale=wl.op_scale, text_tokens=X,
+                              placement=ops.Placement(F, P, None))
+    bufs = [torch.empty_like(t) for t in (q, k, v)]
+    placement.permute([q, k, v], bufs, F, P, X)
+    ot = ops.pisa_pg_attention(bufs[0], bufs[1], bufs[2], wl.density, block_size=wl.block_size,
+                               scale=wl.op_scale, text_tokens=X)
+    ref = torch.empty_like(ot)
+    placement.permute([ot], [ref], F, P, X, inverse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
 
 
 # ------------------------------------------------------------ text segment --

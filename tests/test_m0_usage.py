@@ -18,7 +18,7 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
-@pytest.mark.parametrize("src", ["sparse_attn.hip", "block_stats.hip"])
+@pytest.mark.parametrize("src", ["sparse_attn.hip", "block_stats.hip", "select.hip"])
 def test_only_the_dma_load_touches_m0(src, tmp_path):
     out = tmp_path / (src + ".s")
     cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",

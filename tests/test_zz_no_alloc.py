@@ -50,16 +50,3 @@ def test_noalloc_equals_workspace_entry_two_calls(device):
     ref2, got2 = run_both(small, text_valid=37, gamma="consistent", seed=1)
     assert torch.equal(ref2.view(torch.int16), got2.view(torch.int16)), "call 2 differs from pasa_sparse_attn"
     assert not torch.isnan(got2.float()).any()
-
-
-def test_noalloc_rejects_shapes_above_the_scratch(device):
-    wl = small_workload(WORKLOADS["c2"], heads=40, grid=WORKLOADS["c2"].grid, block_size=64)
-    lib = _lib.load()
-    need = lib.pasa_sparse_attn_workspace_bytes(40, wl.seq_len, 0, 128, 64, 32)
-    assert need > _lib.NOALLOC_SCRATCH_BYTES
-    say(f"[noalloc] c2 at block 64 needs {need} bytes: rejected before any launch")
-    tiny = torch.zeros(16, device=device, dtype=torch.int32)
-    p = tiny.data_ptr()
-    rc = lib.pasa_sparse_attn_noalloc(p, p, p, p, p, p, p, p, p, 0.1, 40, wl.seq_len, 0, 0, 128, 64, 32, 118, 1, 0,
-                                      None)
-    assert rc == -8 and b"static scratch" in lib.pasa_last_error()
