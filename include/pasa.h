@@ -14,7 +14,16 @@
  * slices of [T, D].  Reference interface cited per entry point; paths are
  * relative to the reference tree (ZHANGWENTAI/PASA).
  *
- * Text segment (text_len > 0, head_dim 128 only): the last text_len rows of each
+ * Shapes.  The tuned gfx950 kernels take bf16 q, k, v (fp16 at head_dim 128), head_dim
+ * 64 or 128, block_size 64 or 128 and (attention) group_size 32.  pasa_block_stats,
+ * pasa_select, pasa_sparse_attn, pasa_sparse_attn_noalloc and pasa_dense_attn also take
+ * every other shape the reference does (group_pisa_attention.py:307-398: any float dtype,
+ * any group size, any power-of-two block size): fp32, bf16 or fp16 inputs, head_dim
+ * 1 .. 128, block_size a power of two in [16, 256], group_size 1 .. 2^20, on the
+ * any-shape kernels (the same mathematics in plain VALU arithmetic, for completeness
+ * rather than speed).  The pack / packed / placed entry points take the tuned shapes only.
+ *
+ * Text segment (text_len > 0; head_dim 128 on the tuned kernels): the last text_len rows of each
  * slice are text tokens (HunyuanVideo appends its text last).  Blocks, statistics,
  * selection and the first-order correction cover the first T - text_len rows; every
  * video query block also attends to all text keys exactly, and text query rows
@@ -39,14 +48,14 @@
 extern "C" {
 #endif
 
-#define PASA_ABI_VERSION 10
+#define PASA_ABI_VERSION 11
 
 typedef enum {
   PASA_OK = 0,
   PASA_ERR_NULL_POINTER = -1,   /* a required pointer is NULL                     */
   PASA_ERR_BAD_SHAPE = -2,      /* a size is <= 0, or sizes are inconsistent      */
-  PASA_ERR_HEAD_DIM = -3,       /* head_dim not in {64, 128}                      */
-  PASA_ERR_BLOCK_SIZE = -4,     /* block_size not in {64, 128}                    */
+  PASA_ERR_HEAD_DIM = -3,       /* head_dim not taken by this entry point         */
+  PASA_ERR_BLOCK_SIZE = -4,     /* block_size not taken by this entry point       */
   PASA_ERR_NUM_SELECTED = -5,   /* ns outside [1, NT]                             */
   PASA_ERR_OVERFLOW = -6,       /* an element count overflows the index type     */
   PASA_ERR_DTYPE = -7,          /* dtype not supported by this entry point        */
@@ -54,7 +63,7 @@ typedef enum {
   PASA_ERR_BAD_ARG = -9,        /* scale / density not finite, scale <= 0, ...    */
   PASA_ERR_TEXT_SEGMENT = -10,  /* text segment does not fit the sequence         */
   PASA_ERR_LAUNCH = -11,        /* a kernel launch failed (hipGetLastError)       */
-  PASA_ERR_GROUP_SIZE = -12,    /* group_size not supported (GPU path: 32)        */
+  PASA_ERR_GROUP_SIZE = -12,    /* group_size not taken by this entry point       */
   PASA_ERR_TOO_MANY_BLOCKS = -13 /* NT above the select kernel's limit (4096)     */
 } pasa_status_t;
 
@@ -108,8 +117,8 @@ int pasa_permute(const void* src0, const void* src1, const void* src2,
  *   hnorm[j] = || sum_t (k_t - kc[j]) v_t^T ||_F                        (fp32 [BH,NT])
  *   hgroup[g] = (1/G) * sum_{j in group g, j < NT} H_j                 (fp32 [BH,NG,D,D])
  * with NG = ceil(NT / G).  H_j is never materialised in memory.
- * dtype: PASA_DTYPE_BF16, or PASA_DTYPE_F16 at head_dim 128 (q, k, v; the statistics
- * are fp32 either way).
+ * dtype: PASA_DTYPE_BF16, PASA_DTYPE_F16 or PASA_DTYPE_F32 (q, k, v; the statistics
+ * are fp32 either way); shapes as described at the top.
  * Replaces: fused_chunk_reduce group_pisa_attention.py:268-288 (kernel :66-129,
  *   sqrt at :287) and compute_h_group :291-301. */
 int pasa_block_stats(const void* q, const void* k, const void* v,
@@ -173,12 +182,14 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
  * denominator, sum p_j * n_j) is not rescaled when the running max rises;
  * gamma_literal = 0 rescales it with A and L.
  * scale: the natural-log softmax scale s (> 0); scores use s*log2(e) in base 2
- * and the first-order term uses s.  Group size is 32 on this path.
- * dtype: PASA_DTYPE_BF16, or PASA_DTYPE_F16 at head_dim 128 (q, k, v, o and the
- * packed phase-2 operands; P is rounded to the same type before P.V, as the
- * reference casts it to v's dtype).
+ * and the first-order term uses s.
+ * dtype: PASA_DTYPE_BF16, PASA_DTYPE_F16 or PASA_DTYPE_F32 (q, k, v, o; kc, vc and
+ * hgroup are rounded to that type where the reference stores them in it, and P is
+ * rounded to it before P.V, as the reference casts it to v's dtype; fp32 calls round
+ * nothing); shapes as described at the top.
  * workspace: >= pasa_sparse_attn_workspace_bytes(...) bytes (packed phase-2
- * operands, written by this call).
+ * operands, written by this call; 0 bytes and NULL allowed for shapes outside the
+ * tuned ones, whose kernel reads kc, vc and hgroup directly).
  * Replaces: pisa_pg_fwd_kernel group_pisa_attention.py:135-262, launched at :380-396. */
 int pasa_sparse_attn(const void* q, const void* k, const void* v,
                      const float* kc, const float* vc, const float* hgroup,
@@ -287,7 +298,8 @@ int pasa_sparse_attn_packed_placed(const void* q, const void* k, const void* v, 
  * (every key block exact; no statistics, selection or correction).  With a text
  * segment (text_len > 0) the attention is block-diagonal over [0, seq_len -
  * text_len + text_valid) and the padding rows after it, the cu_seqlens semantics
- * of the dense HunyuanVideo path.  bf16 or fp16, head_dim 128; no workspace.
+ * of the dense HunyuanVideo path.  bf16 or fp16 at head_dim 128 on the tuned kernel;
+ * fp32, bf16 or fp16 at head_dim 1 .. 128 otherwise; no workspace.
  * Replaces: the dense warm-up branch of the processors, flash_attention /
  * F.scaled_dot_product_attention (svg/models/wan/attention.py:299-301, :378-379;
  * svg/models/hyvideo/attention.py:450-476, :671-672). */

@@ -84,7 +84,7 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i64, _dbl, _vp]),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # Size of the static device array behind pasa_sparse_attn_noalloc (PASA_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 64 << 20

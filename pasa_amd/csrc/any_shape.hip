@@ -1,0 +1,461 @@
+// The PISA-PG path for shapes the tuned kernels do not take: fp32 q, k, v; any head
+// dim up to 128; any group size; block sizes 16 .. 256.  Same mathematics, plain VALU
+// arithmetic, one WG per (slice, group) or per (slice, 64-row query tile).
+//
+// Reference: svg/kernels/triton/group_pisa_attention.py
+//   k2_block_stats_any   fused_chunk_reduce_kernel :66-129 (+ sqrt :287) and
+//                        compute_h_group :291-301
+//   k3_scores_any        the selection scores :365-371
+//   k4_sparse_attn_any   pisa_pg_fwd_kernel :135-262
+// The reference accepts any float dtype (o = torch.empty_like(v), :380; statistics
+// stored like q, :275-278), any group size (:312) and any power-of-two block size
+// (:311; Triton's tl.arange needs a power of two).  These kernels round where the
+// reference rounds for 16-bit inputs (kc, vc and Hbar in the input type at their use,
+// P and P-bar cast to it before their products, the output store) and not at all for
+// fp32 inputs, so an fp32 call is the reference's mathematics in fp32.
+//
+// Layout of a query tile: 64 rows, four lanes per row (lane & 3 owns features
+// 32 (lane & 3) .. + 31); a row's dot products are reduced over its four lanes with two
+// xor shuffles, which give all four lanes the same bits.
+#include "common.h"
+#include "kernels.h"
+
+namespace pasa {
+
+namespace {
+
+// Element access for the three input types.  round(x): x rounded to the type and back.
+struct F32E {
+  __device__ static float load(const void* p, int64_t i) { return ((const float*)p)[i]; }
+  __device__ static float round(float x) { return x; }
+  __device__ static void store(void* p, int64_t i, float x) { ((float*)p)[i] = x; }
+};
+struct Bf16E {
+  __device__ static float load(const void* p, int64_t i) {
+    return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+  }
+  __device__ static float round(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+  __device__ static void store(void* p, int64_t i, float x) { ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_bits(x); }
+};
+struct F16E {
+  __device__ static float load(const void* p, int64_t i) { return (float)((const _Float16*)p)[i]; }
+  __device__ static float round(float x) { return (float)(_Float16)x; }
+  __device__ static void store(void* p, int64_t i, float x) { ((_Float16*)p)[i] = (_Float16)x; }
+};
+
+constexpr int kAnyChunk = 32;   // rows of a staged K/V chunk
+constexpr int kAnyLd = 129;     // LDS row stride (floats): feature columns of one row
+constexpr int kAnyTile = 64;    // query rows per attention workgroup
+
+// Sum of x over the four lanes of a row (lanes 4r .. 4r + 3): identical on all four.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __shfl_xor(x, 1, 4);
+  x += __shfl_xor(x, 2, 4);
+  return x;
+}
+
+}  // namespace
+
+// ---- block statistics ---------------------------------------------------------
+// One workgroup (256 threads) per (group of G key blocks, slice); the group's blocks in
+// ascending order.  Thread t owns the entries i = t + 256 m (m < ceil(D*D / 256)) of the
+// D x D moment, (d, e) = (i / D, i % D): H_j[d][e] = sum_t k_t[d] v_t[e] - kbar_j[d] V^_j[e]
+// (:106-107), accumulated over 32-row chunks staged in LDS.  Threads t < D own column t
+// of the block sums of q, k and v.  The group sum adds H_j in block order, then / G.
+template <typename EL>
+__global__ __launch_bounds__(256) void k2_block_stats_any(const void* __restrict__ q, const void* __restrict__ k,
+                                                          const void* __restrict__ v, float* __restrict__ qc,
+                                                          float* __restrict__ kc, float* __restrict__ vc,
+                                                          float* __restrict__ hnorm, float* __restrict__ hgroup,
+                                                          int T, int Tslice, int D, int BT, int NT, int G) {
+  constexpr int CH = kAnyChunk, LD = kAnyLd, MMAX = 128 * 128 / 256;
+  __shared__ float ks[CH * LD];
+  __shared__ float vs[CH * LD];
+  __shared__ float kbar[128];
+  __shared__ float vhat[128];
+  __shared__ float red[4];
+  const int g = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int NG = (NT + G - 1) / G;
+  const int DD = D * D;
+  const int64_t base = (int64_t)bh * Tslice * D;
+  // (d, e) of entry m, stepped from m = 0: i advances by 256.
+  const int d0 = tid / D, e0 = tid - (tid / D) * D;
+  const int dstep = 256 / D, estep = 256 - (256 / D) * D;
+  float gacc[MMAX];
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m) gacc[m] = 0.f;
+  const int j1 = min(NT, (g + 1) * G);
+  for (int j = g * G; j < j1; ++j) {
+    const int r0 = j * BT;
+    const int n = min(BT, T - r0);
+    float hacc[MMAX];
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) hacc[m] = 0.f;
+    float qs = 0.f, ksum = 0.f, vsum = 0.f;
+    for (int c0 = 0; c0 < n; c0 += CH) {
+      const int cn = min(CH, n - c0);
+      __syncthreads();  // the previous chunk's reads are done
+      for (int i = tid; i < cn * D; i += 256) {
+        const int t = i / D;
+        const int d = i - t * D;
+        const int64_t off = base + (int64_t)(r0 + c0 + t) * D + d;
+        ks[t * LD + d] = EL::load(k, off);
+        vs[t * LD + d] = EL::load(v, off);
+      }
+      __syncthreads();
+      if (tid < D) {
+        for (int t = 0; t < cn; ++t) {
+          ksum += ks[t * LD + tid];
+          vsum += vs[t * LD + tid];
+          qs += EL::load(q, base + (int64_t)(r0 + c0 + t) * D + tid);
+        }
+      }
+      int d = d0, e = e0;
+#pragma unroll
+      for (int m = 0; m < MMAX; ++m) {
+        if (tid + 256 * m < DD) {
+          float a = 0.f;
+          for (int t = 0; t < cn; ++t) a = fmaf(ks[t * LD + d], vs[t * LD + e], a);
+          hacc[m] += a;
+        }
+        d += dstep;
+        e += estep;
+        if (e >= D) {
+          e -= D;
+          ++d;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < D) {
+      const float kb = ksum / (float)n;
+      kbar[tid] = kb;
+      vhat[tid] = vsum;
+      const int64_t so = ((int64_t)bh * NT + j) * D + tid;
+      qc[so] = qs / (float)n;  // :101
+      kc[so] = kb;             // :102
+      vc[so] = vsum;           // :103 (a sum, not a mean)
+    }
+    __syncthreads();
+    float nsq = 0.f;
+    int d = d0, e = e0;
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      if (tid + 256 * m < DD) {
+        const float h = hacc[m] - kbar[d] * vhat[e];  // :107
+        nsq = fmaf(h, h, nsq);
+        gacc[m] += h;
+      }
+      d += dstep;
+      e += estep;
+      if (e >= D) {
+        e -= D;
+        ++d;
+      }
+    }
+    nsq = wave_sum(nsq);
+    if ((tid & 63) == 0) red[tid >> 6] = nsq;
+    __syncthreads();
+    if (tid == 0) hnorm[(int64_t)bh * NT + j] = sqrt_rn((red[0] + red[1]) + (red[2] + red[3]));  // :110, :287
+  }
+  // hbar_g = (1/G) sum over the group, the missing blocks of the last group counting as zeros (:294-299).
+  float* hg = hgroup + ((int64_t)bh * NG + g) * DD;
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m)
+    if (tid + 256 * m < DD) hg[tid + 256 * m] = gacc[m] / (float)G;
+}
+
+// ---- selection scores -----------------------------------------------------------
+// score[I][j] = sum_d qc[I][d] * fl(scale * kc[j][d]) + log(hnorm[j] + 1e-6) [+ noise[j]],
+// one thread per score, features in ascending order.
+__global__ __launch_bounds__(256) void k3_scores_any(const float* __restrict__ qc, const float* __restrict__ kc,
+                                                     const float* __restrict__ hnorm, const float* __restrict__ noise,
+                                                     float scale, int use_cov_bias, float* __restrict__ scores, int NT,
+                                                     int D) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int I = blockIdx.y;
+  const int bh = blockIdx.z;
+  if (j >= NT) return;
+  const float* qi = qc + ((int64_t)bh * NT + I) * D;
+  const float* kj = kc + ((int64_t)bh * NT + j) * D;
+  float acc = 0.f;
+  for (int d = 0; d < D; ++d) acc = fmaf(qi[d], mul_rn(scale, kj[d]), acc);
+  float bias = 0.f;
+  if (use_cov_bias) {
+    bias = logf(hnorm[(int64_t)bh * NT + j] + 1e-6f);
+    if (noise) bias = bias + noise[(int64_t)bh * NT + j];
+  }
+  scores[((int64_t)bh * NT + I) * NT + j] = acc + bias;
+}
+
+// ---- attention -----------------------------------------------------------------
+// One workgroup per 64-row query tile of a slice.  Video tiles (a block of BT rows is
+// ceil(BT / 64) tiles) visit the selected key blocks in ascending order (every block
+// when `all`), then the prompt keys [T, T + text_valid); then phase 2 over the groups
+// (not when `all`).  Text tiles attend densely within their segment ([0, seg) for the
+// prompt rows, [seg, T + text) for the padding rows).  Keys go in chunks of 32 staged in
+// LDS, each chunk one online-softmax step (exact: rescaled whenever a row's max rises).
+template <typename EL>
+__global__ __launch_bounds__(256) void k4_sparse_attn_any(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
+    const float* __restrict__ kc, const float* __restrict__ vc, const float* __restrict__ hgroup,
+    const uint32_t* __restrict__ selmask, void* __restrict__ o, float scale, float c, int T, int text,
+    int text_valid, int D, int BT, int NT, int G, int NG, int NW, int gamma_literal, int all) {
+  constexpr int CH = kAnyChunk, LD = kAnyLd, TR = kAnyTile;
+  static_assert(2 * CH * LD >= TR * LD, "an Hbar slab of 64 rows fits the K/V chunk buffers");
+  __shared__ float kv[2 * CH * LD];  // K chunk, V chunk; phase 2: 64 rows of Hbar
+  __shared__ float qsh[TR * LD];     // the tile's q rows
+  float* ks = kv;
+  float* vs = kv + CH * LD;
+  const int tid = threadIdx.x;
+  const int r = tid >> 2;
+  const int qd = tid & 3;
+  const int bh = blockIdx.y;
+  const int Ttot = T + text;
+  const int seg = T + text_valid;
+  const int tpb = (BT + TR - 1) / TR;
+  const int nvt = NT * tpb;
+  int tile = blockIdx.x;
+  int row0, rows, I = -1, kbeg = 0, kend = 0;
+  if (tile < nvt) {
+    I = tile / tpb;
+    const int sub = tile - I * tpb;
+    row0 = I * BT + sub * TR;
+    rows = min(TR, min(BT - sub * TR, T - row0));
+  } else {
+    tile -= nvt;
+    const int ptiles = (text_valid + TR - 1) / TR;
+    if (tile < ptiles) {
+      row0 = T + tile * TR;
+      rows = min(TR, seg - row0);
+      kbeg = 0;
+      kend = seg;
+    } else {
+      row0 = seg + (tile - ptiles) * TR;
+      rows = min(TR, Ttot - row0);
+      kbeg = seg;
+      kend = Ttot;
+    }
+  }
+  if (rows <= 0) return;  // a video tile past the last block's rows
+  const int64_t sbase = (int64_t)bh * Ttot * D;
+  for (int i = tid; i < rows * D; i += 256) {
+    const int rr = i / D;
+    const int d = i - rr * D;
+    qsh[rr * LD + d] = EL::load(q, sbase + (int64_t)(row0 + rr) * D + d);
+  }
+  __syncthreads();
+  const bool live = r < rows;
+  float qp[32], op[32];
+#pragma unroll
+  for (int dd = 0; dd < 32; ++dd) {
+    const int d = qd * 32 + dd;
+    qp[dd] = (live && d < D) ? qsh[r * LD + d] : 0.f;
+    op[dd] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f, gam = 0.f;
+
+  // Keys [key0, key0 + cn), cn <= 32, all valid: one online-softmax step (:174-186).
+  auto chunk = [&](int key0, int cn) __attribute__((always_inline)) {
+    __syncthreads();
+    for (int i = tid; i < cn * D; i += 256) {
+      const int t = i / D;
+      const int d = i - t * D;
+      const int64_t off = sbase + (int64_t)(key0 + t) * D + d;
+      ks[t * LD + d] = EL::load(k, off);
+      vs[t * LD + d] = EL::load(v, off);
+    }
+    __syncthreads();
+    float x[CH];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+      float a = 0.f;
+      if (t < cn) {
+#pragma unroll
+        for (int dd = 0; dd < 32; ++dd)
+          if (qd * 32 + dd < D) a = fmaf(qp[dd], ks[t * LD + qd * 32 + dd], a);
+      }
+      a = quad_sum(a);
+      x[t] = t < cn ? a * c : -INFINITY;
+      mx = fmaxf(mx, x[t]);
+    }
+    const float mn = fmaxf(m, mx);
+    const float al = fast_exp2(m - mn);  // 0 on the first step
+    l *= al;
+#pragma unroll
+    for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+      if (t < cn) {
+        const float p = fast_exp2(x[t] - mn);
+        l += p;
+        const float pr = EL::round(p);  // P cast to v's type before P.V (:185)
+#pragma unroll
+        for (int dd = 0; dd < 32; ++dd)
+          if (qd * 32 + dd < D) op[dd] = fmaf(pr, vs[t * LD + qd * 32 + dd], op[dd]);
+      }
+    }
+    m = mn;
+  };
+  auto keys = [&](int a, int b) __attribute__((always_inline)) {
+    for (int k0 = a; k0 < b; k0 += CH) chunk(k0, min(CH, b - k0));
+  };
+
+  if (I >= 0) {
+    const uint32_t* mrow = all ? nullptr : selmask + ((int64_t)bh * NT + I) * NW;
+    if (all) {
+      keys(0, T);
+    } else {
+      for (int w = 0; w < NW; ++w) {
+        uint32_t bits = mrow[w];
+        while (bits) {
+          const int j = 32 * w + __builtin_ctz(bits);
+          bits &= bits - 1u;
+          keys(j * BT, min(T, (j + 1) * BT));
+        }
+      }
+    }
+    keys(T, seg);  // the prompt keys, exact for every video row
+    if (!all) {
+      // Phase 2 (:212-253): per group, the blocks not selected.
+      const int last_len = T - (NT - 1) * BT;
+      const float* kcb = kc + (int64_t)bh * NT * D;
+      const float* vcb = vc + (int64_t)bh * NT * D;
+      const float* hgb = hgroup + (int64_t)bh * NG * D * D;
+      auto selected = [&](int j) { return (mrow[j >> 5] >> (j & 31)) & 1u; };
+      auto sbar = [&](int j) __attribute__((always_inline)) {  // c q . kbar_j, kbar in the input type (:216-217)
+        float a = 0.f;
+#pragma unroll
+        for (int dd = 0; dd < 32; ++dd)
+          if (qd * 32 + dd < D) a = fmaf(qp[dd], EL::round(kcb[(int64_t)j * D + qd * 32 + dd]), a);
+        return quad_sum(a) * c;
+      };
+      for (int g = 0; g < NG; ++g) {
+        const int j0 = g * G;
+        const int j1 = min(NT, j0 + G);
+        int napprox = 0;
+        for (int j = j0; j < j1; ++j) napprox += selected(j) ? 0 : 1;
+        if (napprox == 0) continue;  // nothing approximated: alpha = 1 and no contribution
+        float gm = -INFINITY;
+        for (int j = j0; j < j1; ++j)
+          if (!selected(j)) gm = fmaxf(gm, sbar(j));
+        const float mn = fmaxf(m, gm);
+        const float al = fast_exp2(m - mn);
+        l *= al;
+        if (!gamma_literal) gam *= al;  // the literal form never rescales Gamma (:231-235)
+#pragma unroll
+        for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
+        m = mn;
+        float ps = 0.f;
+        for (int j = j0; j < j1; ++j) {
+          if (selected(j)) continue;
+          const float p = fast_exp2(sbar(j) - m);
+          ps += p;
+          gam += p * (float)(j == NT - 1 ? last_len : BT);  // :242-243
+          const float pr = EL::round(p);
+#pragma unroll
+          for (int dd = 0; dd < 32; ++dd)
+            if (qd * 32 + dd < D) op[dd] = fmaf(pr, EL::round(vcb[(int64_t)j * D + qd * 32 + dd]), op[dd]);
+        }
+        // First order (:246-253): r = q . Hbar_g (Hbar in q's type), o += r * (sum p * scale).
+        float rr[32];
+#pragma unroll
+        for (int dd = 0; dd < 32; ++dd) rr[dd] = 0.f;
+        for (int d0 = 0; d0 < D; d0 += TR) {
+          const int dn = min(TR, D - d0);
+          __syncthreads();
+          for (int i = tid; i < dn * D; i += 256) {
+            const int dr = i / D;
+            const int e = i - dr * D;
+            kv[dr * LD + e] = EL::round(hgb[((int64_t)g * D + d0 + dr) * D + e]);
+          }
+          __syncthreads();
+          for (int dr = 0; dr < dn; ++dr) {
+            const float qv = qsh[r * LD + d0 + dr];
+#pragma unroll
+            for (int dd = 0; dd < 32; ++dd)
+              if (qd * 32 + dd < D) rr[dd] = fmaf(qv, kv[dr * LD + qd * 32 + dd], rr[dd]);
+          }
+        }
+        const float f = ps * scale;
+#pragma unroll
+        for (int dd = 0; dd < 32; ++dd) op[dd] = fmaf(rr[dd], f, op[dd]);
+      }
+    }
+  } else {
+    keys(kbeg, kend);
+  }
+  // o = A / (L + Gamma) (:258-259), stored in the input type (:262).
+  if (live) {
+    const float den = l + gam;
+#pragma unroll
+    for (int dd = 0; dd < 32; ++dd) {
+      const int e = qd * 32 + dd;
+      if (e < D) EL::store(o, sbase + (int64_t)(row0 + r) * D + e, op[dd] / den);
+    }
+  }
+}
+
+namespace {
+
+template <typename F>
+hipError_t by_dtype(int dtype, F&& f) {
+  switch (dtype) {
+    case kAnyF32: f(F32E{}); break;
+    case kAnyBf16: f(Bf16E{}); break;
+    case kAnyF16: f(F16E{}); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_block_stats_any(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
+                                  float* hnorm, float* hgroup, int bh, int T, int Tslice, int D, int BT, int G,
+                                  int dtype, hipStream_t stream) {
+  if (D < 1 || D > 128 || BT < 1 || G < 1) return hipErrorInvalidValue;
+  const int NT = (T + BT - 1) / BT;
+  const int NG = (NT + G - 1) / G;
+  const dim3 grid(NG, bh);
+  return by_dtype(dtype, [&](auto el) {
+    hipLaunchKernelGGL(k2_block_stats_any<decltype(el)>, grid, dim3(256), 0, stream, q, k, v, qc, kc, vc, hnorm,
+                       hgroup, T, Tslice, D, BT, NT, G);
+  });
+}
+
+hipError_t launch_scores_any(const float* qc, const float* kc, const float* hnorm, const float* noise, float scale,
+                             int use_cov_bias, float* scores, int bh, int NT, int D, hipStream_t stream) {
+  if (D < 1 || D > 128) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k3_scores_any, dim3((NT + 255) / 256, NT, bh), dim3(256), 0, stream, qc, kc, hnorm, noise,
+                     scale, use_cov_bias, scores, NT, D);
+  return hipGetLastError();
+}
+
+int64_t sparse_attn_any_tiles(int T, int text, int text_valid, int BT) {
+  const int64_t NT = (T + BT - 1) / BT;
+  const int64_t tpb = (BT + kAnyTile - 1) / kAnyTile;
+  return NT * tpb + (text_valid + kAnyTile - 1) / kAnyTile + (text - text_valid + kAnyTile - 1) / kAnyTile;
+}
+
+hipError_t launch_sparse_attn_any(const void* q, const void* k, const void* v, const float* kc, const float* vc,
+                                  const float* hgroup, const uint32_t* selmask, void* o, float scale, int bh, int T,
+                                  int text, int text_valid, int D, int BT, int G, int gamma_literal, int all,
+                                  int dtype, hipStream_t stream) {
+  if (D < 1 || D > 128 || BT < 1 || G < 1 || text_valid < 0 || text_valid > text) return hipErrorInvalidValue;
+  if (!all && (kc == nullptr || vc == nullptr || hgroup == nullptr || selmask == nullptr)) return hipErrorInvalidValue;
+  const int NT = (T + BT - 1) / BT;
+  const int NG = (NT + G - 1) / G;
+  const int NW = (NT + 31) / 32;
+  const dim3 grid((unsigned)sparse_attn_any_tiles(T, text, text_valid, BT), bh);
+  const float c = scale * kLog2e;
+  return by_dtype(dtype, [&](auto el) {
+    hipLaunchKernelGGL(k4_sparse_attn_any<decltype(el)>, grid, dim3(256), 0, stream, q, k, v, kc, vc, hgroup,
+                       selmask, o, scale, c, T, text, text_valid, D, BT, NT, G, NG, NW, gamma_literal, all);
+  });
+}
+
+}  // namespace pasa

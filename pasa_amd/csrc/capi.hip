@@ -164,6 +164,46 @@ static int check_attn_dtype(int dtype, int64_t head_dim, const char* what) {
   return fail(PASA_ERR_DTYPE, "%s: dtype %d is not bf16 or fp16", what, dtype);
 }
 
+// The tuned kernels' shapes: bf16 (fp16 at head_dim 128) q, k, v, head_dim 64 or 128, block
+// size 64 or 128.  Every other shape the entry points accept (fp32 inputs, head dims 1 ..
+// 128, block sizes 16 .. 256) runs on the any-shape kernels (any_shape.hip).
+static bool tuned_shape(int dtype, int64_t head_dim, int64_t block_size) {
+  return (head_dim == 64 || head_dim == 128) && (block_size == 64 || block_size == 128) &&
+         (dtype == PASA_DTYPE_BF16 || (dtype == PASA_DTYPE_F16 && head_dim == 128));
+}
+
+// ... and the tuned attention kernels also need group size 32, and a text segment only at
+// head_dim 128.
+static bool tuned_attn_shape(int dtype, int64_t head_dim, int64_t block_size, int64_t group_size,
+                             int64_t text_len) {
+  return tuned_shape(dtype, head_dim, block_size) && group_size == 32 && (text_len == 0 || head_dim == 128);
+}
+
+static int check_any_dtype(int dtype, const char* what) {
+  if (dtype == PASA_DTYPE_BF16 || dtype == PASA_DTYPE_F16 || dtype == PASA_DTYPE_F32) return PASA_OK;
+  return fail(PASA_ERR_DTYPE, "%s: dtype %d is not bf16, fp16 or fp32", what, dtype);
+}
+
+// The any-shape kernels: head_dim 1 .. 128, block size a power of two in [16, 256] (the
+// reference's Triton kernels need a power of two, and tl.dot at least 16), group size
+// 1 .. 2^20, a text segment that leaves at least one blocked row.
+static int check_any_shape(int64_t bh, int64_t seq_len, int64_t text_len, int64_t head_dim, int64_t block_size,
+                           int64_t group_size, const char* what) {
+  if (head_dim < 1 || head_dim > 128)
+    return fail(PASA_ERR_HEAD_DIM, "%s: head_dim %lld not in [1, 128]", what, (long long)head_dim);
+  if (block_size < 16 || block_size > 256 || (block_size & (block_size - 1)))
+    return fail(PASA_ERR_BLOCK_SIZE, "%s: block_size %lld is not a power of two in [16, 256]", what,
+                (long long)block_size);
+  if (group_size <= 0 || group_size > 1 << 20)
+    return fail(PASA_ERR_GROUP_SIZE, "%s: group_size %lld must be in [1, 2^20]", what, (long long)group_size);
+  int rc;
+  if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
+  if (text_len < 0 || text_len >= seq_len)
+    return fail(PASA_ERR_TEXT_SEGMENT, "%s: text_len=%lld must be in [0, seq_len=%lld)", what, (long long)text_len,
+                (long long)seq_len);
+  return PASA_OK;
+}
+
 static int block_stats_impl(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
                             float* hnorm, float* hgroup, int64_t bh, int64_t seq_len, int64_t text_len,
                             int64_t head_dim, int64_t block_size, int64_t group_size, int dtype,
@@ -171,6 +211,17 @@ static int block_stats_impl(const void* q, const void* k, const void* v, float* 
                             size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
   int rc;
+  if (rm == nullptr && !tuned_shape(dtype, head_dim, block_size)) {
+    if ((rc = check_any_dtype(dtype, "pasa_block_stats"))) return rc;
+    if ((rc = check_any_shape(bh, seq_len, text_len, head_dim, block_size, group_size, "pasa_block_stats")))
+      return rc;
+    const int64_t ng = cdiv(cdiv(seq_len - text_len, block_size), group_size);
+    if (ng > 65535 * 1024LL) return fail(PASA_ERR_OVERFLOW, "pasa_block_stats: too many groups");
+    return launch_status(pasa::launch_block_stats_any(q, k, v, qc, kc, vc, hnorm, hgroup, (int)bh,
+                                                      (int)(seq_len - text_len), (int)seq_len, (int)head_dim,
+                                                      (int)block_size, (int)group_size, dtype, (hipStream_t)stream),
+                         "pasa_block_stats");
+  }
   if ((rc = check_head_dim(head_dim))) return rc;
   if ((rc = check_attn_dtype(dtype, head_dim, "pasa_block_stats"))) return rc;
   if ((rc = check_block(block_size))) return rc;
@@ -296,7 +347,8 @@ int pasa_select(const float* qc, const float* kc, const float* hnorm, const floa
   if (use_cov_bias && !hnorm) return fail(PASA_ERR_NULL_POINTER, "pasa_select: hnorm is NULL with use_cov_bias");
   int rc;
   if ((rc = check_select_shape(bh, num_blocks))) return rc;
-  if ((rc = check_head_dim(head_dim))) return rc;
+  if (head_dim < 1 || head_dim > 128)
+    return fail(PASA_ERR_HEAD_DIM, "pasa_select: head_dim %lld not in [1, 128]", (long long)head_dim);
   if (!std::isfinite(scale)) return fail(PASA_ERR_BAD_ARG, "scale must be finite");
   const int64_t ns = pasa_num_selected(density, num_blocks);
   if (ns < 0) return (int)ns;
@@ -308,9 +360,14 @@ int pasa_select(const float* qc, const float* kc, const float* hnorm, const floa
     scores = (float*)workspace;
   }
   hipStream_t s = (hipStream_t)stream;
-  rc = launch_status(pasa::launch_scores(qc, kc, hnorm, noise, (float)scale, use_cov_bias, scores, (int)bh,
-                                         (int)num_blocks, (int)head_dim, s),
-                     "pasa_select(scores)");
+  if (head_dim == 64 || head_dim == 128)
+    rc = launch_status(pasa::launch_scores(qc, kc, hnorm, noise, (float)scale, use_cov_bias, scores, (int)bh,
+                                           (int)num_blocks, (int)head_dim, s),
+                       "pasa_select(scores)");
+  else
+    rc = launch_status(pasa::launch_scores_any(qc, kc, hnorm, noise, (float)scale, use_cov_bias, scores, (int)bh,
+                                               (int)num_blocks, (int)head_dim, s),
+                       "pasa_select(scores)");
   if (rc) return rc;
   return launch_status(pasa::launch_topk(scores, (int)bh, (int)num_blocks, (int)ns, idx, selmask, s),
                        "pasa_select(topk)");
@@ -375,15 +432,29 @@ int pasa_pack_phase2(const float* kc, const float* vc, const float* hgroup, void
 }
 
 // idx is not read (the kernels visit the blocks of selmask), so it may be NULL.
+// tuned: NULL for the packed entry points (the tuned shapes only); else receives whether
+// the call runs on the tuned kernels or on the any-shape ones.
 static int check_attn_args(const void* q, const void* k, const void* v, const int32_t* idx,
                            const uint32_t* selmask, const void* o, double scale, int64_t bh,
                            int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim,
-                           int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype) {
+                           int64_t block_size, int64_t group_size, int64_t ns, int gamma_literal, int dtype,
+                           bool* tuned = nullptr) {
   (void)idx;
   if (!q || !k || !v || !selmask || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
   int rc;
-  if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
-  if ((rc = check_attn_dtype(dtype, head_dim, "pasa_sparse_attn"))) return rc;
+  if (tuned != nullptr && !tuned_attn_shape(dtype, head_dim, block_size, group_size, text_len)) {
+    *tuned = false;
+    if ((rc = check_any_dtype(dtype, "pasa_sparse_attn"))) return rc;
+    if ((rc = check_any_shape(bh, seq_len, text_len, head_dim, block_size, group_size, "pasa_sparse_attn")))
+      return rc;
+    if (pasa::sparse_attn_any_tiles((int)(seq_len - text_len), (int)text_len, (int)text_len,
+                                    (int)block_size) + 2 > kMaxI32)
+      return fail(PASA_ERR_OVERFLOW, "grid too large");
+  } else {
+    if (tuned != nullptr) *tuned = true;
+    if ((rc = check_attn_shape(bh, seq_len, text_len, head_dim, block_size, group_size))) return rc;
+    if ((rc = check_attn_dtype(dtype, head_dim, "pasa_sparse_attn"))) return rc;
+  }
   if (text_valid < 0 || text_valid > text_len)
     return fail(PASA_ERR_TEXT_SEGMENT, "text_valid=%lld must be in [0, text_len=%lld]", (long long)text_valid,
                 (long long)text_len);
@@ -441,9 +512,16 @@ int pasa_sparse_attn(const void* q, const void* k, const void* v, const float* k
                      int dtype, void* workspace, size_t workspace_bytes, void* stream) {
   if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn: NULL pointer");
   int rc;
+  bool tuned = true;
   if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, text_valid, head_dim,
-                            block_size, group_size, ns, gamma_literal, dtype)))
+                            block_size, group_size, ns, gamma_literal, dtype, &tuned)))
     return rc;
+  if (!tuned)  // the any-shape kernel reads kc, vc, hgroup directly: no workspace
+    return launch_status(pasa::launch_sparse_attn_any(q, k, v, kc, vc, hgroup, selmask, o, (float)scale, (int)bh,
+                                                      (int)(seq_len - text_len), (int)text_len, (int)text_valid,
+                                                      (int)head_dim, (int)block_size, (int)group_size,
+                                                      gamma_literal, 0, dtype, (hipStream_t)stream),
+                         "pasa_sparse_attn");
   if ((rc = check_pack(workspace, workspace_bytes, bh, seq_len, text_len, head_dim, block_size, group_size)))
     return rc;
   if ((rc = pasa_pack_phase2(kc, vc, hgroup, workspace, workspace_bytes, bh, seq_len, text_len, head_dim,
@@ -515,9 +593,16 @@ int pasa_sparse_attn_noalloc(const void* q, const void* k, const void* v, const 
                              int gamma_literal, int dtype, void* stream) {
   if (!kc || !vc || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_sparse_attn_noalloc: NULL pointer");
   int rc;
+  bool tuned = true;
   if ((rc = check_attn_args(q, k, v, idx, selmask, o, scale, bh, seq_len, text_len, text_valid, head_dim,
-                            block_size, group_size, ns, gamma_literal, dtype)))
+                            block_size, group_size, ns, gamma_literal, dtype, &tuned)))
     return rc;
+  if (!tuned)  // the any-shape kernel needs no scratch
+    return launch_status(pasa::launch_sparse_attn_any(q, k, v, kc, vc, hgroup, selmask, o, (float)scale, (int)bh,
+                                                      (int)(seq_len - text_len), (int)text_len, (int)text_valid,
+                                                      (int)head_dim, (int)block_size, (int)group_size,
+                                                      gamma_literal, 0, dtype, (hipStream_t)stream),
+                         "pasa_sparse_attn_noalloc");
   const size_t need = pasa_sparse_attn_workspace_bytes(bh, seq_len, text_len, head_dim, block_size, group_size);
   if (need > kScratchBytes)
     return fail(PASA_ERR_WORKSPACE,
@@ -536,8 +621,23 @@ int pasa_dense_attn(const void* q, const void* k, const void* v, void* o, double
                     int64_t seq_len, int64_t text_len, int64_t text_valid, int64_t head_dim, int dtype,
                     void* stream) {
   if (!q || !k || !v || !o) return fail(PASA_ERR_NULL_POINTER, "pasa_dense_attn: NULL pointer");
-  if (head_dim != 128) return fail(PASA_ERR_HEAD_DIM, "pasa_dense_attn: head_dim %lld != 128", (long long)head_dim);
   int rc;
+  if (!(head_dim == 128 && (dtype == PASA_DTYPE_BF16 || dtype == PASA_DTYPE_F16))) {
+    // fp32 inputs or head dims other than 128: the any-shape kernel with every block exact
+    if ((rc = check_any_dtype(dtype, "pasa_dense_attn"))) return rc;
+    if ((rc = check_any_shape(bh, seq_len, text_len, head_dim, 64, 1, "pasa_dense_attn"))) return rc;
+    if (text_valid < 0 || text_valid > text_len)
+      return fail(PASA_ERR_TEXT_SEGMENT, "text_valid=%lld must be in [0, text_len=%lld]", (long long)text_valid,
+                  (long long)text_len);
+    if (!std::isfinite(scale) || !(scale > 0.0)) return fail(PASA_ERR_BAD_ARG, "scale must be finite and > 0");
+    if (pasa::sparse_attn_any_tiles((int)(seq_len - text_len), (int)text_len, (int)text_valid, 64) > kMaxI32)
+      return fail(PASA_ERR_OVERFLOW, "grid too large");
+    return launch_status(pasa::launch_sparse_attn_any(q, k, v, nullptr, nullptr, nullptr, nullptr, o, (float)scale,
+                                                      (int)bh, (int)(seq_len - text_len), (int)text_len,
+                                                      (int)text_valid, (int)head_dim, 64, 1, 1, 1, dtype,
+                                                      (hipStream_t)stream),
+                         "pasa_dense_attn");
+  }
   if ((rc = check_attn_dtype(dtype, head_dim, "pasa_dense_attn"))) return rc;
   if ((rc = check_bh_seq(bh, seq_len, head_dim))) return rc;
   if ((rc = check_slice_bytes(seq_len, head_dim, 2))) return rc;

@@ -55,6 +55,25 @@ hipError_t launch_sparse_attn(const void* q, const void* k, const void* v, const
 hipError_t launch_dense_attn(const void* q, const void* k, const void* v, void* o, float scale, int bh,
                              int T, int text, int text_valid, bool f16, hipStream_t stream);
 
+// ---- any-shape path (any_shape.hip) ----------------------------------------------
+// fp32, bf16 or fp16 q, k, v (dtype: kAnyBf16 / kAnyF16 / kAnyF32, the pasa_dtype_t
+// values); head dim 1 .. 128; any block size and group size.  Outputs as the tuned
+// kernels' (fp32 statistics; o in the input type).
+constexpr int kAnyBf16 = 0;
+constexpr int kAnyF16 = 1;
+constexpr int kAnyF32 = 2;
+hipError_t launch_block_stats_any(const void* q, const void* k, const void* v, float* qc, float* kc, float* vc,
+                                  float* hnorm, float* hgroup, int bh, int T, int Tslice, int D, int BT, int G,
+                                  int dtype, hipStream_t stream);
+hipError_t launch_scores_any(const float* qc, const float* kc, const float* hnorm, const float* noise, float scale,
+                             int use_cov_bias, float* scores, int bh, int NT, int D, hipStream_t stream);
+// all: dense (every key block exact, no correction; kc, vc, hgroup, selmask unused).
+hipError_t launch_sparse_attn_any(const void* q, const void* k, const void* v, const float* kc, const float* vc,
+                                  const float* hgroup, const uint32_t* selmask, void* o, float scale, int bh, int T,
+                                  int text, int text_valid, int D, int BT, int G, int gamma_literal, int all,
+                                  int dtype, hipStream_t stream);
+int64_t sparse_attn_any_tiles(int T, int text, int text_valid, int BT);  // grid.x of launch_sparse_attn_any
+
 // ---- K5: processor prologue (RMSNorm + rotary embedding + head-major layout) ----
 constexpr int kNormHead = 1;       // RMSNorm over each head's D channels, weight [D]
 constexpr int kNormRow = 2;        // RMSNorm over the token's H*D channels, weight [H*D]

@@ -58,18 +58,32 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise ValueError(f"q, k, v must have one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
 
 
-def _check_stats(stats: "BlockStats", q: torch.Tensor, block_size: int, text_tokens: int) -> None:
-    """The statistics must be block_stats' for q's shape and this block size: the pack
-    kernel reads kc, vc and hgroup with the sizes derived from q."""
+def _check_stats(stats: "BlockStats", q: torch.Tensor, block_size: int, text_tokens: int,
+                 group_size: int = GROUP_SIZE) -> None:
+    """The statistics must be block_stats' for q's shape, this block size and group size: the
+    kernels read kc, vc and hgroup with the sizes derived from q."""
     B, H, T, D = q.shape
     NT = math.ceil((T - int(text_tokens)) / block_size)
-    NG = math.ceil(NT / GROUP_SIZE)
+    NG = math.ceil(NT / group_size)
     want = {"kc": (B, H, NT, D), "vc": (B, H, NT, D), "hgroup": (B, H, NG, D, D)}
     for name, shape in want.items():
         t = getattr(stats, name)
         if tuple(t.shape) != shape or t.dtype != torch.float32:
             raise ValueError(f"stats.{name} must be float32 {list(shape)} for block_size {block_size}, "
                              f"got {t.dtype} {tuple(t.shape)}")
+
+
+def tuned_shape(dtype: torch.dtype, head_dim: int, block_size: int, group_size: int = GROUP_SIZE,
+                text_tokens: int = 0) -> bool:
+    """Whether an attention call of this shape runs on the tuned gfx950 kernels: bf16 (or fp16
+    at head_dim 128), head_dim 64 or 128, block size 64 or 128, group size 32, and a text
+    segment only at head_dim 128.  Every other shape the library takes (fp32 inputs, head dims
+    1 .. 128, block sizes 16 .. 256 that are powers of two, any group size) runs on the
+    any-shape kernels: the same mathematics with plain VALU arithmetic, for completeness
+    rather than speed."""
+    return (head_dim in (64, 128) and block_size in (64, 128) and group_size == GROUP_SIZE
+            and (dtype == torch.bfloat16 or (dtype == torch.float16 and head_dim == 128))
+            and (text_tokens == 0 or head_dim == 128))
 
 
 def num_selected(density: float, num_blocks: int) -> int:
@@ -220,7 +234,7 @@ def select_from_scores(scores: torch.Tensor, ns: int) -> Selection:
 
 def pack_phase2(q: torch.Tensor, stats: BlockStats, block_size: int = 64, text_tokens: int = 0) -> torch.Tensor:
     """Phase-2 operands (kbar, V^T, Hbar^T) per (slice, group), in q's dtype (bf16 or
-    fp16), as K4 stages them in LDS."""
+    fp16), as the tuned K4 stages them in LDS (tuned shapes only: ``tuned_shape``)."""
     if q.dim() != 4:
         raise ValueError(f"q must be [B, H, T, D], got {tuple(q.shape)}")
     _check_stats(stats, q, block_size, text_tokens)
@@ -298,13 +312,33 @@ def sparse_attn_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pack: 
 def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockStats,
                 sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
                 out: Optional[torch.Tensor] = None, text_tokens: int = 0,
-                text_valid: Optional[int] = None, placement: Optional[Placement] = None) -> torch.Tensor:
+                text_valid: Optional[int] = None, placement: Optional[Placement] = None,
+                group_size: int = GROUP_SIZE) -> torch.Tensor:
     """Exact attention over the selected blocks plus the per-group first-order
     correction of the rest (reference pisa_pg_fwd_kernel :135-262); with
     ``text_tokens``, the prompt keys are exact for every video query block and the
     text rows are dense within their segment.  With ``placement`` (q, k, v frame-major)
     the call reads q's rows through the placement map and k, v from the token-major view
-    ``stats`` holds, and stores o frame-major."""
+    ``stats`` holds, and stores o frame-major.  ``group_size`` must be the one ``stats``
+    was computed with.  Shapes outside ``tuned_shape`` run on the any-shape kernels
+    (``pasa_sparse_attn`` reads the statistics directly; no pack, no placement)."""
+    _check_qkv(q, k, v)
+    B, H, T, D = q.shape
+    if placement is None and not tuned_shape(q.dtype, D, block_size, group_size, text_tokens):
+        _check_stats(stats, q, block_size, text_tokens, group_size)
+        _check_device(q, k, v, stats.kc, stats.vc, stats.hgroup)
+        if gamma not in ("literal", "consistent"):
+            raise ValueError("gamma must be 'literal' or 'consistent'")
+        _check_selection(sel, q, block_size, text_tokens)
+        o = _check_out(v, out)
+        _lib.call("pasa_sparse_attn", q.data_ptr(), k.data_ptr(), v.data_ptr(), stats.kc.data_ptr(),
+                  stats.vc.data_ptr(), stats.hgroup.data_ptr(), _ptr(sel.idx), sel.selmask.data_ptr(),
+                  o.data_ptr(), float(scale), B * H, T, int(text_tokens),
+                  int(text_tokens if text_valid is None else text_valid), D, block_size, int(group_size), sel.ns,
+                  int(gamma == "literal"), _DTYPES.get(q.dtype, -1), None, 0, _stream(q))
+        return o
+    if group_size != GROUP_SIZE:
+        raise ValueError(f"the placed call runs on the tuned kernels, which use group_size={GROUP_SIZE}")
     pack = pack_phase2(q, stats, block_size, text_tokens)
     if placement is not None:  # the token-major k, v K2 wrote; the output goes back frame-major
         if stats.k_tm is None or stats.v_tm is None:
@@ -317,13 +351,13 @@ def sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockS
 def sparse_attn_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats: BlockStats,
                         sel: Selection, scale: float, block_size: int = 64, gamma: str = "literal",
                         out: Optional[torch.Tensor] = None, text_tokens: int = 0,
-                        text_valid: Optional[int] = None) -> torch.Tensor:
+                        text_valid: Optional[int] = None, group_size: int = GROUP_SIZE) -> torch.Tensor:
     """``sparse_attn`` through ``pasa_sparse_attn_noalloc``: the phase-2 pack lives in the
     library's static device array, so with ``out`` given the call allocates nothing
     (for code under HIP graph capture).  Shapes whose pack exceeds
     ``_lib.NOALLOC_SCRATCH_BYTES`` raise PasaError (PASA_ERR_WORKSPACE)."""
     _check_qkv(q, k, v)
-    _check_stats(stats, q, block_size, text_tokens)
+    _check_stats(stats, q, block_size, text_tokens, group_size)
     _check_device(q, k, v, stats.kc, stats.vc, stats.hgroup)
     if gamma not in ("literal", "consistent"):
         raise ValueError("gamma must be 'literal' or 'consistent'")
@@ -333,7 +367,7 @@ def sparse_attn_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats
     _lib.call("pasa_sparse_attn_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), stats.kc.data_ptr(),
               stats.vc.data_ptr(), stats.hgroup.data_ptr(), _ptr(sel.idx), sel.selmask.data_ptr(),
               o.data_ptr(), float(scale), B * H, T, int(text_tokens),
-              int(text_tokens if text_valid is None else text_valid), D, block_size, GROUP_SIZE, sel.ns,
+              int(text_tokens if text_valid is None else text_valid), D, block_size, int(group_size), sel.ns,
               int(gamma == "literal"), _DTYPES.get(q.dtype, -1), _stream(q))
     return o
 
@@ -341,11 +375,11 @@ def sparse_attn_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, stats
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
                     text_tokens: int = 0, text_valid: Optional[int] = None,
                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Dense softmax attention on K4's exact-tile path (bf16 or fp16, head_dim 128), for the
-    processors' warm-up layers (reference flash_attention, svg/models/wan/attention.py:299-301,
+    """Dense softmax attention on K4's exact-tile path (bf16 or fp16 at head_dim 128; fp32 and
+    other head dims up to 128 on the any-shape kernel), for the processors' warm-up layers (reference flash_attention, svg/models/wan/attention.py:299-301,
     svg/models/hyvideo/attention.py:459-476).  With ``text_tokens`` / ``text_valid``
     the attention is block-diagonal over [0, T - text_tokens + text_valid) and the
-    rest (the dense HunyuanVideo path's cu_seqlens).  q, k, v: [B, H, T, 128]."""
+    rest (the dense HunyuanVideo path's cu_seqlens).  q, k, v: [B, H, T, D]."""
     _check_qkv(q, k, v)
     _check_device(q, k, v)
     B, H, T, D = q.shape
@@ -388,7 +422,10 @@ def pisa_pg_attention(
 ):
     """PISA with per-group first-order correction (drop-in for reference :307-398).
 
-    q, k, v: [B, H, T, D] contiguous bf16 or fp16, D <= 128, on a ROCm device; returns o like v.
+    q, k, v: [B, H, T, D] contiguous bf16, fp16 or fp32, D <= 128, on a ROCm device; returns o
+    like v.  ``group_size`` may be any positive integer and ``block_size`` any power of two in
+    [16, 256], as in the reference (:311-312); shapes outside ``tuned_shape`` run on the
+    any-shape kernels.
     ``timestep``, ``verbose`` and ``prompt_token_length`` do not change the math
     (as in the reference, where ``prompt_token_length`` is documented but unused).
     ``use_random`` adds one N(0,1) draw per key block to the selection score; pass
@@ -416,11 +453,11 @@ def pisa_pg_attention(
     unpadded math; the padded output features are dropped."""
     _check_qkv(q, k, v)
     B, H, T, D = q.shape
-    if group_size != GROUP_SIZE:
-        raise ValueError(f"the gfx950 kernels use group_size={GROUP_SIZE}")
     scale = D ** -0.5 if scale is None else scale
     Dk = kernel_head_dim(D, q.dtype, text_tokens, placement is not None)
-    if Dk != D:
+    # Zero-pad to the tuned kernels' head dim when that makes the call tuned; other calls
+    # (fp32, other group or block sizes) run at their own head dim on the any-shape kernels.
+    if Dk != D and (placement is not None or tuned_shape(q.dtype, Dk, block_size, group_size, text_tokens)):
         pad = lambda t: torch.nn.functional.pad(t, (0, Dk - D)).contiguous()
         o = pisa_pg_attention(pad(q), pad(k), pad(v), density, timestep, block_size, group_size, scale,
                               use_cov_bias, use_random, verbose, prompt_token_length, noise=noise, gamma=gamma,
@@ -437,4 +474,4 @@ def pisa_pg_attention(
         print(f"NT={NT}, N_GROUPS={stats.hgroup.shape[2]}, GROUP_SIZE={group_size}")
         print(f"top_k={sel.ns}, density={density}")
     return sparse_attn(q, k, v, stats, sel, scale, block_size, gamma, text_tokens=text_tokens,
-                       text_valid=text_valid, placement=placement)
+                       text_valid=text_valid, placement=placement, group_size=group_size)

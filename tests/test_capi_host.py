@@ -100,10 +100,14 @@ def stats(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(q=None), -1), (dict(hg=None), -1), (dict(dtype=2), -7), (dict(dtype=1, D=64), -7), (dict(dtype=5), -7),
-    (dict(D=96), -3), (dict(BT=32), -4), (dict(T=0), -2), (dict(bh=-1), -2), (dict(G=0), -12),
+    (dict(q=None), -1), (dict(hg=None), -1), (dict(dtype=3), -7), (dict(dtype=-1), -7), (dict(dtype=5), -7),
+    (dict(D=129), -3), (dict(D=0), -3), (dict(BT=48), -4), (dict(BT=512), -4), (dict(BT=8), -4),
+    (dict(T=0), -2), (dict(bh=-1), -2), (dict(G=0), -12),
     (dict(T=1 << 31), -6), (dict(T=(1 << 24) - 100), -6),
-    (dict(text=-1), -10), (dict(text=1000), -10), (dict(text=10, D=64), -10),
+    (dict(text=-1), -10), (dict(text=1000), -10),
+    # the any-shape route (fp32, head dims other than 64 / 128, block sizes 16 .. 256)
+    (dict(dtype=2, G=0), -12), (dict(D=96, BT=24), -4), (dict(dtype=2, text=1000), -10),
+    (dict(D=96, bh=70000), -6), (dict(dtype=2, T=0), -2), (dict(dtype=2, q=None), -1),
 ])
 def test_block_stats_validation(lib, kw, code):
     assert stats(lib, **kw) == code
@@ -122,7 +126,7 @@ def select(lib, **kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(qc=None), -1), (dict(mask=None), -1), (dict(idx=None, mask=None), -1), (dict(hn=None), -1),
     (dict(idx=None, nt=0), -2), (dict(nt=0), -2),
-    (dict(nt=5000), -13), (dict(D=32), -3), (dict(scale=float("inf")), -9),
+    (dict(nt=5000), -13), (dict(D=129), -3), (dict(D=0), -3), (dict(scale=float("inf")), -9),
     (dict(density=float("nan")), -9), (dict(scores=None), -8),
     (dict(scores=None, ws=FAKE, wsb=100), -8), (dict(bh=1 << 20), -6),
 ])
@@ -155,13 +159,17 @@ def attn(lib, **kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(o=None), -1), (dict(mask=None), -1), (dict(idx=None, mask=None), -1), (dict(idx=None, D=256), -3),
-    (dict(dtype=2), -7), (dict(dtype=1, D=64, BT=64), -7), (dict(D=256), -3),
-    (dict(BT=256), -4), (dict(G=16), -12), (dict(ns=0), -5), (dict(ns=9), -5),
+    (dict(dtype=3), -7), (dict(dtype=-1), -7), (dict(D=256), -3), (dict(D=0), -3),
+    (dict(BT=512), -4), (dict(BT=100), -4), (dict(G=0), -12), (dict(ns=0), -5), (dict(ns=9), -5),
     (dict(scale=0.0), -9), (dict(scale=-1.0), -9), (dict(scale=float("nan")), -9),
     (dict(lit=2), -9), (dict(ws=None), -8), (dict(wsb=10), -8), (dict(T=0), -2),
     (dict(T=(1 << 24) - 100), -6), (dict(text=1000), -10), (dict(text=-3), -10),
-    (dict(text=100, D=64), -10), (dict(text=200, ns=8), -5), (dict(text=100, tv=101), -10),
+    (dict(text=200, ns=8), -5), (dict(text=100, tv=101), -10),
     (dict(text=100, tv=-1), -10), (dict(text=0, tv=1), -10),
+    # the any-shape route: its own shape checks, and the same argument checks
+    (dict(dtype=2, G=0), -12), (dict(G=16, BT=24), -4), (dict(dtype=2, D=200), -3), (dict(G=16, ns=9), -5),
+    (dict(dtype=2, scale=0.0), -9), (dict(G=16, lit=2), -9), (dict(dtype=2, text=1000), -10),
+    (dict(D=64, text=100, tv=101), -10), (dict(G=16, mask=None), -1), (dict(dtype=2, T=0), -2),
 ])
 def test_sparse_attn_validation(lib, kw, code):
     assert attn(lib, **kw) == code
@@ -179,8 +187,8 @@ def attn_noalloc(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(o=None), -1), (dict(kc=None), -1), (dict(dtype=2), -7), (dict(D=256), -3), (dict(BT=256), -4),
-    (dict(G=16), -12), (dict(ns=9), -5), (dict(scale=0.0), -9), (dict(lit=2), -9),
+    (dict(o=None), -1), (dict(kc=None), -1), (dict(dtype=3), -7), (dict(D=256), -3), (dict(BT=512), -4),
+    (dict(G=0), -12), (dict(ns=9), -5), (dict(scale=0.0), -9), (dict(lit=2), -9), (dict(dtype=2, G=0), -12),
     (dict(text=100, tv=101), -10),
     # the pack of 1261 slice-groups (53,248 bytes each) exceeds the 64 MiB static scratch
     (dict(bh=1261, T=4096, ns=1), -8),
@@ -279,10 +287,13 @@ def test_prologue_validation(lib, kw, code):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(o=None), -1), (dict(q=None), -1), (dict(dtype=2), -7), (dict(D=64), -3), (dict(T=0), -2),
-    (dict(bh=0), -2), (dict(text=1000), -10), (dict(text=-1), -10), (dict(text=10, tv=11), -10),
+    (dict(o=None), -1), (dict(q=None), -1), (dict(dtype=3), -7), (dict(D=129), -3), (dict(D=0), -3),
+    (dict(T=0), -2), (dict(bh=0), -2), (dict(text=1000), -10), (dict(text=-1), -10), (dict(text=10, tv=11), -10),
     (dict(text=10, tv=-1), -10), (dict(scale=0.0), -9), (dict(scale=float("inf")), -9),
     (dict(T=(1 << 24) - 100), -6),
+    # the any-shape route (fp32, head dims other than 128)
+    (dict(dtype=2, text=10, tv=11), -10), (dict(D=64, scale=0.0), -9), (dict(D=64, T=0), -2),
+    (dict(dtype=2, o=None), -1), (dict(D=64, text=1000), -10),
 ])
 def test_dense_attn_validation(lib, kw, code):
     a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, scale=0.1, bh=2, T=1000, text=0, tv=None, D=128, dtype=0)
