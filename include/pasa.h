@@ -64,7 +64,7 @@ typedef enum {
   PASA_ERR_TEXT_SEGMENT = -10,  /* text segment does not fit the sequence         */
   PASA_ERR_LAUNCH = -11,        /* a kernel launch failed (hipGetLastError)       */
   PASA_ERR_GROUP_SIZE = -12,    /* group_size not taken by this entry point       */
-  PASA_ERR_TOO_MANY_BLOCKS = -13 /* NT above the select kernel's limit (4096)     */
+  PASA_ERR_TOO_MANY_BLOCKS = -13 /* NT above 65536, or an index list > 8192 at NT > 4096 */
 } pasa_status_t;
 
 typedef enum {
@@ -154,7 +154,9 @@ size_t pasa_block_stats_workspace_bytes(int64_t bh, int64_t seq_len, int64_t tex
  * key block, shared by all query blocks; used only with use_cov_bias).  scores_out:
  * optional fp32 [BH, NT, NT] output; when NULL the workspace holds the scores.
  * workspace: device buffer of at least pasa_select_workspace_bytes(bh, NT) bytes
- * (may be NULL when scores_out is given).
+ * (may be NULL when scores_out is given).  head_dim 1 .. 128; NT <= 65536 (rows of more
+ * than 4096 blocks take a radix select over the row in memory, whose index list, when
+ * asked for, holds at most 8192 blocks).
  * Replaces: group_pisa_attention.py:365-375. */
 int pasa_select(const float* qc, const float* kc, const float* hnorm, const float* noise,
                 double scale, double density, int use_cov_bias,

@@ -339,6 +339,14 @@ static int check_select_shape(int64_t bh, int64_t nt) {
   return PASA_OK;
 }
 
+// Rows of more than 4096 blocks sort their index list in LDS: at most 8192 indices.
+static int check_index_list(const int32_t* idx, int64_t nt, int64_t ns) {
+  if (idx != nullptr && nt > 4096 && ns > pasa::kMaxLargeSortKeys)
+    return fail(PASA_ERR_TOO_MANY_BLOCKS, "an index list of %lld blocks (of %lld) exceeds %d; pass idx = NULL "
+                "for the selection bitmask alone", (long long)ns, (long long)nt, pasa::kMaxLargeSortKeys);
+  return PASA_OK;
+}
+
 int pasa_select(const float* qc, const float* kc, const float* hnorm, const float* noise,
                 double scale, double density, int use_cov_bias, int32_t* idx, uint32_t* selmask,
                 float* scores_out, void* workspace, size_t workspace_bytes, int64_t bh,
@@ -352,6 +360,7 @@ int pasa_select(const float* qc, const float* kc, const float* hnorm, const floa
   if (!std::isfinite(scale)) return fail(PASA_ERR_BAD_ARG, "scale must be finite");
   const int64_t ns = pasa_num_selected(density, num_blocks);
   if (ns < 0) return (int)ns;
+  if ((rc = check_index_list(idx, num_blocks, ns))) return rc;
   float* scores = scores_out;
   if (!scores) {
     if (!workspace) return fail(PASA_ERR_WORKSPACE, "pasa_select: need scores_out or a workspace");
@@ -379,6 +388,7 @@ int pasa_select_from_scores(const float* scores, int64_t ns, int32_t* idx, uint3
   int rc;
   if ((rc = check_select_shape(bh, num_blocks))) return rc;
   if (ns < 1 || ns > num_blocks) return fail(PASA_ERR_NUM_SELECTED, "ns=%lld not in [1, %lld]", (long long)ns, (long long)num_blocks);
+  if ((rc = check_index_list(idx, num_blocks, ns))) return rc;
   return launch_status(pasa::launch_topk(scores, (int)bh, (int)num_blocks, (int)ns, idx, selmask, (hipStream_t)stream),
                        "pasa_select_from_scores");
 }

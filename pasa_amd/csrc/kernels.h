@@ -10,7 +10,9 @@
 
 namespace pasa {
 
-constexpr int kMaxSelectBlocks = 4096;  // NT limit of the top-k kernel (LDS-resident row)
+constexpr int kMaxSelectBlocks = 1 << 16;  // NT limit of the selection (k3_topk: NT <= 4096 in
+                                            // registers; k3_topk_large beyond)
+constexpr int kMaxLargeSortKeys = 8192;    // index list of k3_topk_large: NS <= 8192 (LDS sort)
 
 hipError_t launch_permute(const void* s0, const void* s1, const void* s2, void* d0, void* d1,
                           void* d2, int ntens, int bh, int S, int F, int P, int ctx, int row_bytes,

@@ -491,6 +491,115 @@ hipError_t launch_scores(const float* qc, const float* kc, const float* hnorm, c
   return hipGetLastError();
 }
 
+// Rows longer than k3_topk holds in registers (NT > 4096): one workgroup of 256 threads per
+// row, the row read from memory (L2) in index order.  The NS-th largest ordered score T is
+// found by a radix select, 8 bits per pass from the top, with a 256-bin histogram in LDS of
+// the scores in the current bucket (integer counts: the order of the LDS atomic adds does
+// not matter).  Every score above T is selected and, of those equal to T, the lowest
+// indices, ranked by a workgroup prefix count of the ties in index order.  With IDX the
+// picked keys (score << 32 | ~index) are packed into LDS in index order and sorted
+// descending (bitonic, NSP = pow2 >= NS <= 8192: 64 KB of dynamic LDS).
+template <bool IDX>
+__global__ __launch_bounds__(256) void k3_topk_large(const float* __restrict__ scores, int NT, int NS, int NSP,
+                                                     int NW, int32_t* __restrict__ idx,
+                                                     uint32_t* __restrict__ selmask) {
+  extern __shared__ uint64_t sel[];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wcount[4];
+  __shared__ uint32_t s_bin, s_above;
+  const int row = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const float* srow = scores + ((int64_t)bh * NT + row) * NT;
+  uint32_t prefix = 0u, fixed = 0u, above = 0u;  // bucket bits so far; #scores above the bucket
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0u;
+    __syncthreads();
+    for (int j = tid; j < NT; j += 256) {
+      const uint32_t o = score_ord(srow[j]);
+      if ((o & fixed) == prefix) atomicAdd(&hist[(o >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t cum = above;
+      int b = 255;
+      for (; b > 0; --b) {
+        if (cum + hist[b] >= (uint32_t)NS) break;
+        cum += hist[b];
+      }
+      s_bin = (uint32_t)b;
+      s_above = cum;
+    }
+    __syncthreads();
+    prefix |= s_bin << shift;
+    fixed |= 255u << shift;
+    above = s_above;
+  }
+  // prefix = T; above = #{scores > T}; the NS - above lowest-index scores equal to T are taken.
+  const uint32_t need = (uint32_t)NS - above;
+  uint32_t* mrow = selmask + ((int64_t)bh * NT + row) * NW;
+  uint32_t ties = 0u, picks = 0u;  // ties and picks in earlier chunks
+  for (int j0 = 0; j0 < NT; j0 += 256) {
+    const int j = j0 + tid;
+    const uint32_t o = j < NT ? score_ord(srow[j]) : 0u;
+    const bool tie = j < NT && o == prefix;
+    const uint64_t tb = ballot(tie);
+    if (lane == 0) wcount[wave] = (uint32_t)__popcll(tb);
+    __syncthreads();
+    uint32_t below = 0u, total = 0u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      below += w < wave ? wcount[w] : 0u;
+      total += wcount[w];
+    }
+    const bool pick = j < NT && (o > prefix || (tie && ties + below + lanes_below(tb) < need));
+    ties += total;
+    const uint64_t pb = ballot(pick);
+    if (lane == 0) {
+      const int w0 = (j0 + 64 * wave) >> 5;
+      if (w0 < NW) mrow[w0] = (uint32_t)pb;
+      if (w0 + 1 < NW) mrow[w0 + 1] = (uint32_t)(pb >> 32);
+    }
+    __syncthreads();  // wcount is rewritten below / in the next chunk
+    if constexpr (IDX) {
+      if (lane == 0) wcount[wave] = (uint32_t)__popcll(pb);
+      __syncthreads();
+      uint32_t pbelow = 0u, ptotal = 0u;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        pbelow += w < wave ? wcount[w] : 0u;
+        ptotal += wcount[w];
+      }
+      if (pick) sel[picks + pbelow + lanes_below(pb)] = ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)j);
+      picks += ptotal;
+      __syncthreads();
+    }
+  }
+  if constexpr (IDX) {
+    for (int i = NS + tid; i < NSP; i += 256) sel[i] = 0ull;
+    __syncthreads();
+    for (int kk = 2; kk <= NSP; kk <<= 1) {
+      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+        for (int p = tid; p < (NSP >> 1); p += 256) {
+          const int i = ((p & ~(jj - 1)) << 1) | (p & (jj - 1));
+          const int l = i + jj;
+          const uint64_t a = sel[i];
+          const uint64_t b = sel[l];
+          const bool desc = (i & kk) == 0;
+          const bool swap = desc ? (a < b) : (a > b);
+          sel[i] = swap ? b : a;
+          sel[l] = swap ? a : b;
+        }
+        __syncthreads();
+      }
+    }
+    int32_t* irow = idx + ((int64_t)bh * NT + row) * NS;
+    for (int i = tid; i < NS; i += 256) irow[i] = (int)(0xffffffffu - (uint32_t)(sel[i] & 0xffffffffull));
+  }
+}
+
 hipError_t launch_topk(const float* scores, int bh, int NT, int NS, int32_t* idx,
                        uint32_t* selmask, hipStream_t stream) {
   int NSP = 1;
@@ -498,6 +607,15 @@ hipError_t launch_topk(const float* scores, int bh, int NT, int NS, int32_t* idx
   if (NSP < 2) NSP = 2;
   const int NW = (NT + 31) / 32;
   dim3 grid(NT, bh);
+  if (NT > 4096) {
+    if (idx && NSP > kMaxLargeSortKeys) return hipErrorInvalidValue;
+    if (idx)
+      hipLaunchKernelGGL((k3_topk_large<true>), grid, dim3(256), (size_t)NSP * sizeof(uint64_t), stream, scores, NT,
+                         NS, NSP, NW, idx, selmask);
+    else
+      hipLaunchKernelGGL((k3_topk_large<false>), grid, dim3(256), 0, stream, scores, NT, NS, NSP, NW, idx, selmask);
+    return hipGetLastError();
+  }
   const size_t lds = idx ? (size_t)(NSP + 64) * sizeof(uint64_t) : 0;
 #define PASA_TOPK(K)                                                                                         \
   case K:                                                                                                    \

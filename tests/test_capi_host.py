@@ -126,7 +126,7 @@ def select(lib, **kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(qc=None), -1), (dict(mask=None), -1), (dict(idx=None, mask=None), -1), (dict(hn=None), -1),
     (dict(idx=None, nt=0), -2), (dict(nt=0), -2),
-    (dict(nt=5000), -13), (dict(D=129), -3), (dict(D=0), -3), (dict(scale=float("inf")), -9),
+    (dict(nt=70000), -13), (dict(nt=10000, density=0.9), -13), (dict(D=129), -3), (dict(D=0), -3), (dict(scale=float("inf")), -9),
     (dict(density=float("nan")), -9), (dict(scores=None), -8),
     (dict(scores=None, ws=FAKE, wsb=100), -8), (dict(bh=1 << 20), -6),
 ])
@@ -142,7 +142,8 @@ def test_select_from_scores_validation(lib):
     assert f(FAKE, 0, None, FAKE, 1, 10, None) == -5  # idx is optional: the shape checks still run
     assert f(FAKE, 0, FAKE, FAKE, 1, 10, None) == -5
     assert f(FAKE, 11, FAKE, FAKE, 1, 10, None) == -5
-    assert f(FAKE, 3, FAKE, FAKE, 1, 4097, None) == -13
+    assert f(FAKE, 3, FAKE, FAKE, 1, 65537, None) == -13
+    assert f(FAKE, 8193, FAKE, FAKE, 1, 10000, None) == -13   # an index list past the LDS sort
     assert lib.pasa_select_workspace_bytes(2, 10) == 800
     assert lib.pasa_select_workspace_bytes(0, 10) == 0
 

@@ -206,6 +206,30 @@ def test_select_from_scores_bit_exact(device, NT, ns):
     np.testing.assert_array_equal(sel.selmask.cpu().numpy().view(np.uint32), O.selection_mask(want, NT))
 
 
+@pytest.mark.parametrize("NT,ns,BH", [(4097, 410, 2), (5000, 1, 1), (6000, 6000, 1), (9000, 8192, 1)])
+def test_select_from_scores_long_rows_bit_exact(device, NT, ns, BH):
+    """Rows of more than 4096 blocks take the radix select over the row in memory: the same
+    rule (score desc, index asc; -0.0 == +0.0) on constructed ties, bit-exact."""
+    say(f"[K3] select_from_scores (long rows) NT={NT} ns={ns} BH={BH}")
+    g = torch.Generator().manual_seed(NT + ns)
+    s = torch.randn(1, BH, NT, NT, generator=g)
+    s[0, 0] = torch.round(s[0, 0] * 4) / 4            # heavy ties at every rank
+    s[0, 0, 1, ::2] = 0.0
+    s[0, 0, 1, 1::2] = -0.0                           # -0.0 ties with +0.0
+    s[0, 0, 2] = 1.0                                  # an all-equal row
+    sel = ops.select_from_scores(s.to(device), ns)
+    rows = list(range(0, NT, max(1, NT // 300))) + [1, 2, NT - 1]   # the oracle on a sample of rows
+    sub = s[:, :, rows]
+    want = O.topk_indices(sub, ns)
+    np.testing.assert_array_equal(sel.idx.cpu()[:, :, rows].numpy(), want.numpy())
+    np.testing.assert_array_equal(sel.selmask.cpu()[:, :, rows].numpy().view(np.uint32), O.selection_mask(want, NT))
+    # the bitmask alone (the attention call's form) equals the one written with the indices
+    m2 = torch.empty_like(sel.selmask)
+    _lib.call("pasa_select_from_scores", s.to(device).data_ptr(), ns, None, m2.data_ptr(), BH, NT,
+              torch.cuda.current_stream().cuda_stream)
+    assert torch.equal(m2, sel.selmask)
+
+
 @pytest.mark.parametrize("heads,grid,D,BT,density,use_noise", [
     (2, (4, 16, 16), 64, 64, 0.25, False),
     (2, (21, 30, 52), 128, 128, 0.15, True),
@@ -497,6 +521,18 @@ def test_end_to_end_block64_first_and_last_head(device, name, text_valid):
     q, k, v, o, st, idx = run_heads(wl, heads, device, text_valid)
     r = check_end_to_end(o, q, k, v, wl, st, idx, (0, 1), None, f"{name} block 64", text_valid=text_valid)
     say(f"[E2E] {name} block 64: kernel/floor max-abs ratio {r['kernel_over_floor']:.3f}")
+    assert r["kernel_over_floor"] <= 1.5
+
+
+def test_end_to_end_more_than_4096_blocks(device):
+    """A sequence of 4200 key blocks (268,800 tokens at block size 64, one head, density 0.02):
+    the radix-select top-k feeds the tuned attention kernel; checked end to end like c2."""
+    base = WORKLOADS["c2"]
+    wl = dataclasses.replace(base, heads=1, grid=(4, 140, 480), block_size=64, density=0.02)
+    assert wl.num_blocks() == 4200
+    say(f"[E2E] long sequence: T={wl.seq_len}, NT {wl.num_blocks()}, NS {ops.num_selected(wl.density, 4200)}")
+    q, k, v, o, st, idx = run_heads(wl, range(0, 1), device)
+    r = check_end_to_end(o, q, k, v, wl, st, idx, (0,), None, "4200 blocks")
     assert r["kernel_over_floor"] <= 1.5
 
 
