@@ -211,7 +211,8 @@ static int block_stats_impl(const void* q, const void* k, const void* v, float* 
                             size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !qc || !kc || !vc || !hnorm || !hgroup) return fail(PASA_ERR_NULL_POINTER, "pasa_block_stats: NULL pointer");
   int rc;
-  if (rm == nullptr && !tuned_shape(dtype, head_dim, block_size)) {
+  // The tuned statistics kernels take a text segment at head_dim 128 only.
+  if (rm == nullptr && (!tuned_shape(dtype, head_dim, block_size) || (text_len != 0 && head_dim != 128))) {
     if ((rc = check_any_dtype(dtype, "pasa_block_stats"))) return rc;
     if ((rc = check_any_shape(bh, seq_len, text_len, head_dim, block_size, group_size, "pasa_block_stats")))
       return rc;

@@ -118,6 +118,7 @@ ATTN_CASES = [  # heads, T, D, BT, G, density, dtype, gamma, text, text_valid
     (2, 900, 128, 16, 64, 0.1, torch.float32, "literal", 60, None),        # block 16, fp32 text
     (1, 2600, 128, 128, 64, 0.1, torch.bfloat16, "literal", 0, None),      # group size 64
     (1, 1200, 96, 64, 32, 0.25, torch.float32, "consistent", 0, None),
+    (2, 1100, 64, 64, 32, 0.2, torch.bfloat16, "literal", 50, 20),         # a text segment at head_dim 64
 ]
 
 
