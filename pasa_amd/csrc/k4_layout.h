@@ -1,0 +1,33 @@
+// LDS images shared by the D = 128 K4 kernels (k4_sparse_attn_dma and k4w_sparse_attn)
+// and the pack kernel that writes their phase-2 operands.
+#pragma once
+
+#include "common.h"
+
+namespace pasa {
+
+constexpr int kGroup = 32;  // key blocks per group of the first-order correction
+
+// Phase-2 pack image for the D = 128 direct-load kernels, split between their two
+// LDS tile buffers: [Hbar^T: 128 rows x 256 B, XOR layout of a K tile] -> K buffer;
+// [kbar: 32 rows x 256 B, XOR layout][V^ transposed: PadTile<32>] -> V buffer.
+// Both parts are whole multiples of 4 KB, so the waves of a workgroup (four, or two)
+// split their 1 KB direct loads evenly.
+template <int BT>
+struct K4DPack {
+  static constexpr int HT_BYTES = 128 * 256;
+  static constexpr int KB_OFF = 0;                       // within the V-buffer part
+  static constexpr int VT_OFF = 32 * 256;
+  static constexpr int RAW2 = VT_OFF + PadTile<kGroup>::bytes(128);
+  static constexpr int PART2 = (RAW2 + 4095) / 4096 * 4096;
+  static constexpr int BYTES = HT_BYTES + PART2;
+  static_assert(HT_BYTES % 4096 == 0, "pack split");
+};
+
+// Byte offset of element (row, col) in a 256-byte-row tile whose 16-byte chunk c
+// of row r is stored at c ^ (r & 15).
+__host__ __device__ __forceinline__ constexpr int xor_tile_byte(int row, int col) {
+  return row * 256 + ((((col >> 3) ^ row) & 15) << 4) + (col & 7) * 2;
+}
+
+}  // namespace pasa

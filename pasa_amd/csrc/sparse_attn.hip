@@ -47,11 +47,10 @@
 // The D = 128 kernels and k4_pack_xor take that type as a template argument (Bf16 or
 // F16: the MFMA and the rounding of P, the pack and o); the D = 64 ones are bf16.
 #include "common.h"
+#include "k4_layout.h"
 #include "kernels.h"
 
 namespace pasa {
-
-constexpr int kGroup = 32;
 
 template <int D, int BT>
 struct K4Cfg {
@@ -115,28 +114,6 @@ __global__ __launch_bounds__(256) void k4_pack(const float* __restrict__ kc,
     const int e = u - d * D;
     *(uint16_t*)(out + C::PK_HT_OFF + C::PHT::elem_byte(e, d)) = (uint16_t)f32_to_bf16_bits(hb[u]);
   }
-}
-
-// Phase-2 pack image for the D = 128 direct-load kernel, split between its two
-// LDS tile buffers: [Hbar^T: 128 rows x 256 B, XOR layout of a K tile] -> K buffer;
-// [kbar: 32 rows x 256 B, XOR layout][V^ transposed: PadTile<32>] -> V buffer.
-// Both parts are whole multiples of 4 KB, so the four waves of a
-// workgroup split their 1 KB direct loads evenly.
-template <int BT>
-struct K4DPack {
-  static constexpr int HT_BYTES = 128 * 256;
-  static constexpr int KB_OFF = 0;                       // within the V-buffer part
-  static constexpr int VT_OFF = 32 * 256;
-  static constexpr int RAW2 = VT_OFF + PadTile<kGroup>::bytes(128);
-  static constexpr int PART2 = (RAW2 + 4095) / 4096 * 4096;
-  static constexpr int BYTES = HT_BYTES + PART2;
-  static_assert(HT_BYTES % 4096 == 0, "pack split");
-};
-
-// Byte offset of element (row, col) in a 256-byte-row tile whose 16-byte chunk c
-// of row r is stored at c ^ (r & 15).
-__host__ __device__ __forceinline__ constexpr int xor_tile_byte(int row, int col) {
-  return row * 256 + ((((col >> 3) ^ row) & 15) << 4) + (col & 7) * 2;
 }
 
 // One workgroup per (group, slice).  Every output element is written once, as part of
