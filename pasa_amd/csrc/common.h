@@ -100,6 +100,23 @@ __device__ __forceinline__ void dma_load16_lds(u32x4_t rsrc, uint32_t lds_addr, 
                : "memory");
 }
 
+// The same load with the nontemporal cache policy (nt), for data read exactly once: it
+// streams through L2 instead of displacing lines other kernels or workgroups reuse.
+__device__ __forceinline__ void dma_load16_lds_nt(u32x4_t rsrc, uint32_t lds_addr, uint32_t byte_off,
+                                                  uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(byte_off), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory");
+}
+
+// buf_load16 with the nontemporal cache policy (cache-policy operand bit 1: nt on gfx950).
+__device__ __forceinline__ uint4 buf_load16_nt(rsrc_t r, uint32_t byte_off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 2);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
 // Workgroup barrier without a memory fence, so in-flight direct-to-LDS tile loads
 // are not drained (a fenced __syncthreads would wait for them).  It is used only
 // where this wave's preceding LDS reads have been consumed by MFMAs, i.e. have

@@ -1,4 +1,4 @@
-"""The direct-to-LDS tile loads (dma_load16_lds in pasa_amd/csrc/common.h) write m0
+"""The direct-to-LDS tile loads (dma_load16_lds and dma_load16_lds_nt in pasa_amd/csrc/common.h) write m0
 inside inline assembly, which the compiler cannot see.  That is safe only while no
 kernel also contains a compiler-generated m0 user (whose m0 value the compiler may
 set once and hoist).  This compiles the kernels that use the load to gfx950
