@@ -169,13 +169,13 @@ __global__ __launch_bounds__(256) void k2_block_stats_any(const void* __restrict
 
 // ---- selection scores -----------------------------------------------------------
 // score[I][j] = sum_d qc[I][d] * fl(scale * kc[j][d]) + log(hnorm[j] + 1e-6) [+ noise[j]],
-// one thread per score, features in ascending order.
+// one thread per score, features in ascending order; one row per grid x index.
 __global__ __launch_bounds__(256) void k3_scores_any(const float* __restrict__ qc, const float* __restrict__ kc,
                                                      const float* __restrict__ hnorm, const float* __restrict__ noise,
                                                      float scale, int use_cov_bias, float* __restrict__ scores, int NT,
                                                      int D) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  const int I = blockIdx.y;
+  const int j = blockIdx.y * 256 + threadIdx.x;
+  const int I = blockIdx.x;  // the row on grid x: NT may exceed grid y's 65,535
   const int bh = blockIdx.z;
   if (j >= NT) return;
   const float* qi = qc + ((int64_t)bh * NT + I) * D;
@@ -430,7 +430,7 @@ hipError_t launch_block_stats_any(const void* q, const void* k, const void* v, f
 hipError_t launch_scores_any(const float* qc, const float* kc, const float* hnorm, const float* noise, float scale,
                              int use_cov_bias, float* scores, int bh, int NT, int D, hipStream_t stream) {
   if (D < 1 || D > 128) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k3_scores_any, dim3((NT + 255) / 256, NT, bh), dim3(256), 0, stream, qc, kc, hnorm, noise,
+  hipLaunchKernelGGL(k3_scores_any, dim3(NT, (NT + 255) / 256, bh), dim3(256), 0, stream, qc, kc, hnorm, noise,
                      scale, use_cov_bias, scores, NT, D);
   return hipGetLastError();
 }
