@@ -67,3 +67,19 @@ def test_kernel_head_dim():
     for d in (0, 129, 256):
         with pytest.raises(ValueError, match="head_dim"):
             ops.kernel_head_dim(d, bf)
+
+
+def test_tuned_shape_routing_table():
+    """Which calls run on the tuned kernels (the rule capi.hip's tuned_attn_shape applies): bf16 at
+    head_dim 64 or 128, fp16 at 128, block size 64 or 128, group size 32, a text segment only at
+    head_dim 128.  Everything else goes to the any-shape kernels."""
+    bf, f16, f32 = torch.bfloat16, torch.float16, torch.float32
+    tuned = [(bf, 64, 64, 32, 0), (bf, 128, 128, 32, 0), (bf, 128, 64, 32, 256), (f16, 128, 128, 32, 0),
+             (f16, 128, 64, 32, 100)]
+    other = [(f32, 128, 128, 32, 0), (f32, 64, 64, 32, 0), (f16, 64, 64, 32, 0), (bf, 96, 128, 32, 0),
+             (bf, 128, 32, 32, 0), (bf, 128, 256, 32, 0), (bf, 128, 128, 16, 0), (bf, 64, 64, 32, 10),
+             (bf, 48, 64, 32, 0)]
+    for dt, d, bt, g, text in tuned:
+        assert ops.tuned_shape(dt, d, bt, g, text), (dt, d, bt, g, text)
+    for dt, d, bt, g, text in other:
+        assert not ops.tuned_shape(dt, d, bt, g, text), (dt, d, bt, g, text)
