@@ -399,3 +399,34 @@ def test_block_stats_workspace(lib):
     assert lib.pasa_block_stats_ws(*args, F16 + 4, need, None) == -9                  # misaligned
     a2 = [FAKE] * 7 + [None] + [12, 32760, 0, 128, 128, 32, 0]
     assert lib.pasa_block_stats_ws(*a2, F16, need, None) == -1                        # hgroup NULL
+
+
+def header_arity():
+    """Number of parameters of every prototype in the header (0 for `(void)`)."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    arity = {}
+    for name, params in re.findall(r"\b(pasa_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = params.strip()
+        arity[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return arity
+
+
+def test_integration_stub_matches_header():
+    """The ctypes stub INTEGRATION.md shows a maintainer declares every argument list with as
+    many entries as the header's prototype has parameters."""
+    doc = (ROOT / "INTEGRATION.md").read_text()
+    stub = doc[doc.index("## 3. Binding the C ABI directly"):]
+    stub = stub[stub.index("```python"):]
+    stub = stub[:stub.index("```", 9)]
+    aliases = {"_vp": ctypes.c_void_p, "_i64": ctypes.c_int64, "_int": ctypes.c_int,
+               "_dbl": ctypes.c_double, "_sz": ctypes.c_size_t}
+    arity = header_arity()
+    checked = 0
+    for name, both, expr in re.findall(r"_lib\.(pasa_[a-z0-9_]+)\.argtypes(, _lib\.\1\.restype)? = (.+)", stub):
+        if both:  # "argtypes, restype = [...], type": keep the list
+            expr = expr[:expr.rindex("]") + 1]
+        lst = eval(expr, {}, dict(aliases))
+        assert name in arity, name
+        assert len(lst) == arity[name], (name, len(lst), arity[name])
+        checked += 1
+    assert checked >= 5, checked
