@@ -1,0 +1,116 @@
+"""Seeded random shapes through the attention stage (tuned and any-shape routes) against the
+CPU oracle on the GPU's own statistics and selection (run with -m gpu).
+
+The other GPU tests pick their shapes by hand; these draw combinations nobody picked: ragged
+lengths, text segments with and without padding (text_valid 0 .. text_tokens), block sizes
+16 .. 256, group sizes 8 .. 64, densities up to 1.0, both Gamma forms, bf16, fp16 and fp32,
+head dims 48 .. 128.  The draw is fixed by a seed, so every case id names the same shape on
+every run.  Criteria as in test_gpu_any_shape.py: fp32 is held to the north_star bound itself,
+16-bit inputs to 1.5x the error of the oracle run at the reference's own roundings (+ one ulp).
+Each case also checks run-to-run bit equality and that the allocation-free entry gives the
+same bits."""
+import math
+import random
+import sys
+
+import pytest
+import torch
+
+from oracle import pisa_oracle as O
+from pasa_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.999
+BOUND = 2e-2
+
+
+def draw_cases(seed: int, n: int, tuned_only: bool):
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        if tuned_only:
+            D = rng.choice([128, 128, 128, 64])
+            BT = rng.choice([64, 128])
+            G = 32
+            dtype = rng.choice(["bf16", "f16"]) if D == 128 else "bf16"
+        else:
+            D = rng.choice([128, 128, 64, 96, 80, 48, 112])
+            BT = rng.choice([64, 128, 32, 256, 16])
+            G = rng.choice([32, 32, 16, 64, 8])
+            dtype = rng.choice(["bf16", "bf16", "f16", "f32"])
+        heads = rng.choice([1, 2])
+        T = rng.randint(max(BT, 200), 6000 if tuned_only else 3500)
+        text = rng.choice([0, 0, rng.randint(1, min(300, T // 4))])
+        if tuned_only and D != 128:
+            text = 0
+        valid = None if text == 0 or rng.random() < 0.5 else rng.randint(0, text)
+        density = rng.choice([0.05, 0.1, 0.15, 0.25, 0.5, 1.0])
+        gamma = ("literal", "consistent")[i % 2]
+        cases.append((heads, T, D, BT, G, dtype, density, gamma, text, valid))
+    return cases
+
+
+# Plus an empty prompt (text_valid 0: every text row is padding) on each route, which the draw
+# does not reach.
+CASES = (draw_cases(20261202, 16, tuned_only=True) + draw_cases(20261203, 16, tuned_only=False)
+         + [(1, 1500, 128, 64, 32, "bf16", 0.15, "literal", 100, 0),
+            (2, 1300, 128, 128, 32, "f16", 0.25, "consistent", 130, 0),
+            (1, 900, 96, 32, 16, "f32", 0.2, "literal", 70, 0)])
+DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def case_id(c):
+    heads, T, D, BT, G, dtype, density, gamma, text, valid = c
+    return f"H{heads}-T{T}-D{D}-BT{BT}-G{G}-{dtype}-d{density}-{gamma[:3]}-text{text}-valid{valid}"
+
+
+def inputs(heads, T, D, dtype, seed, text=0):
+    """N(0,1) plus a smooth positional component of random amplitude on the video rows of q and k."""
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.arange(T - text, dtype=torch.float32)[:, None]
+    lam = torch.rand(D, generator=g) * 6 + 2
+    phi = torch.rand(D, generator=g) * 2 * math.pi
+    wave = torch.sin(2 * math.pi * pos / lam + phi)
+    q, k, v = (torch.randn(1, heads, T, D, generator=g) for _ in range(3))
+    amp = 0.5 + 2.5 * torch.rand(1, generator=g).item()
+    q[..., : T - text, :] += amp * wave
+    k[..., : T - text, :] += amp * wave
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[case_id(c) for c in CASES])
+def test_random_shape_attention(device, case):
+    heads, T, D, BT, G, dname, density, gamma, text, valid = case
+    dtype = DTYPES[dname]
+    print(f"[random] {case_id(case)} tuned={ops.tuned_shape(dtype, D, BT, G, text)}", flush=True)
+    sys.stdout.flush()
+    q, k, v = inputs(heads, T, D, dtype, seed=T * 131 + D * 7 + BT, text=text)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    scale = D ** -0.5
+    st = ops.block_stats(qd, kd, vd, BT, G, text_tokens=text)
+    sel = ops.select_blocks(st, density, scale)
+    kw = dict(text_tokens=text, text_valid=valid, group_size=G)
+    o = ops.sparse_attn(qd, kd, vd, st, sel, scale, BT, gamma, **kw)
+    o_again = ops.sparse_attn(qd, kd, vd, st, sel, scale, BT, gamma, **kw)
+    o_noalloc = ops.sparse_attn_noalloc(qd, kd, vd, st, sel, scale, BT, gamma, **kw)
+    torch.cuda.synchronize()
+    assert o.dtype == dtype
+    assert torch.equal(o.view(torch.uint8), o_again.view(torch.uint8)), "run-to-run bit equality"
+    assert torch.equal(o.view(torch.uint8), o_noalloc.view(torch.uint8)), "allocation-free entry"
+
+    okw = dict(gamma=gamma, indices=sel.idx.cpu(), text_tokens=text, text_valid=valid)
+    ref = O.pisa_pg_attention(q, k, v, density, BT, G, scale, **okw)
+    m = O.parity_metrics(o.cpu(), ref, torch.bfloat16 if dtype == torch.float32 else dtype)
+    msg = f"[random]   cos={m['cos']:.7f} max_abs/rms={m['max_abs_over_rms']:.3e} excess/rms={m['excess_over_rms']:.3e}"
+    assert m["cos"] >= COS_MIN, m
+    if dtype == torch.float32:
+        print(msg, flush=True)
+        assert m["max_abs_over_rms"] <= BOUND, m
+    else:
+        rp = O.pisa_pg_attention(q, k, v, density, BT, G, scale, ref_precision=dtype, **okw)
+        floor = O.parity_metrics(rp, ref, dtype)
+        print(msg + f" floor max_abs/rms={floor['max_abs_over_rms']:.3e}", flush=True)
+        assert m["excess_over_rms"] <= max(BOUND, 1.5 * floor["excess_over_rms"]), (m, floor)
+        ulp = float(O.ulp(torch.tensor(ref.abs().max().item()), dtype))
+        assert m["max_abs"] <= 1.5 * floor["max_abs"] + ulp, (m, floor)
