@@ -16,7 +16,7 @@
 //
 // Layout of a query tile: 64 rows, four lanes per row (lane & 3 owns features
 // 32 (lane & 3) .. + 31); a row's dot products are reduced over its four lanes with two
-// xor shuffles, which give all four lanes the same bits.
+// DPP quad permutations, which give all four lanes the same bits.
 #include "common.h"
 #include "kernels.h"
 
@@ -44,13 +44,16 @@ struct F16E {
 };
 
 constexpr int kAnyChunk = 32;   // rows of a staged K/V chunk
-constexpr int kAnyLd = 129;     // LDS row stride (floats): feature columns of one row
+constexpr int kAnyLd = 129;     // LDS row stride (floats) of the statistics kernel's chunks
+constexpr int kAnyLdA = 132;    // ... and of the attention kernel's tiles: 16-byte rows, so a
+                                // lane's 32 features are eight ds_read_b128
 constexpr int kAnyTile = 64;    // query rows per attention workgroup
 
-// Sum of x over the four lanes of a row (lanes 4r .. 4r + 3): identical on all four.
+// Sum of x over the four lanes of a row (lanes 4r .. 4r + 3): (x0 + x1) + (x2 + x3) on all
+// four (addition commutes, so every lane gets the same bits), by two DPP quad permutations.
 __device__ __forceinline__ float quad_sum(float x) {
-  x += __shfl_xor(x, 1, 4);
-  x += __shfl_xor(x, 2, 4);
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));  // lane ^ 1
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));  // lane ^ 2
   return x;
 }
 
@@ -197,16 +200,20 @@ __global__ __launch_bounds__(256) void k3_scores_any(const float* __restrict__ q
 // (not when `all`).  Text tiles attend densely within their segment ([0, seg) for the
 // prompt rows, [seg, T + text) for the padding rows).  Keys go in chunks of 32 staged in
 // LDS, each chunk one online-softmax step (exact: rescaled whenever a row's max rises).
+// Feature columns D .. 127 of every LDS row hold zeros (written once, never overwritten),
+// as do a lane's q features past D, so the dot products run over all 32 features of a lane
+// with no per-feature test: the extra terms are 0 * 0.
 template <typename EL>
-__global__ __launch_bounds__(256) void k4_sparse_attn_any(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k4_sparse_attn_any(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ kc, const float* __restrict__ vc, const float* __restrict__ hgroup,
     const uint32_t* __restrict__ selmask, void* __restrict__ o, float scale, float c, int T, int text,
     int text_valid, int D, int BT, int NT, int G, int NG, int NW, int gamma_literal, int all) {
-  constexpr int CH = kAnyChunk, LD = kAnyLd, TR = kAnyTile;
+  constexpr int CH = kAnyChunk, LD = kAnyLdA, TR = kAnyTile;
   static_assert(2 * CH * LD >= TR * LD, "an Hbar slab of 64 rows fits the K/V chunk buffers");
-  __shared__ float kv[2 * CH * LD];  // K chunk, V chunk; phase 2: 64 rows of Hbar
-  __shared__ float qsh[TR * LD];     // the tile's q rows
+  static_assert(LD % 4 == 0, "16-byte LDS rows");
+  __shared__ __attribute__((aligned(16))) float kv[2 * CH * LD];  // K chunk, V chunk; phase 2: 64 rows of Hbar
+  __shared__ __attribute__((aligned(16))) float qsh[TR * LD];     // the tile's q rows
   float* ks = kv;
   float* vs = kv + CH * LD;
   const int tid = threadIdx.x;
@@ -241,20 +248,26 @@ __global__ __launch_bounds__(256) void k4_sparse_attn_any(
   }
   if (rows <= 0) return;  // a video tile past the last block's rows
   const int64_t sbase = (int64_t)bh * Ttot * D;
-  for (int i = tid; i < rows * D; i += 256) {
-    const int rr = i / D;
-    const int d = i - rr * D;
-    qsh[rr * LD + d] = EL::load(q, sbase + (int64_t)(row0 + rr) * D + d);
+  // The tile's q rows, zeros past D and past its last row; the K/V buffers start as zeros.
+  for (int i = tid; i < TR * 128; i += 256) {
+    const int rr = i >> 7;
+    const int d = i & 127;
+    qsh[rr * LD + d] = (rr < rows && d < D) ? EL::load(q, sbase + (int64_t)(row0 + rr) * D + d) : 0.f;
   }
+  for (int i = tid; i < 2 * CH * LD; i += 256) kv[i] = 0.f;
   __syncthreads();
   const bool live = r < rows;
   float qp[32], op[32];
 #pragma unroll
-  for (int dd = 0; dd < 32; ++dd) {
-    const int d = qd * 32 + dd;
-    qp[dd] = (live && d < D) ? qsh[r * LD + d] : 0.f;
-    op[dd] = 0.f;
+  for (int d4 = 0; d4 < 8; ++d4) {
+    const float4 qq = *reinterpret_cast<const float4*>(qsh + r * LD + qd * 32 + 4 * d4);
+    qp[4 * d4] = qq.x;
+    qp[4 * d4 + 1] = qq.y;
+    qp[4 * d4 + 2] = qq.z;
+    qp[4 * d4 + 3] = qq.w;
   }
+#pragma unroll
+  for (int dd = 0; dd < 32; ++dd) op[dd] = 0.f;
   float m = -INFINITY, l = 0.f, gam = 0.f;
 
   // Keys [key0, key0 + cn), cn <= 32, all valid: one online-softmax step (:174-186).
@@ -268,35 +281,66 @@ __global__ __launch_bounds__(256) void k4_sparse_attn_any(
       vs[t * LD + d] = EL::load(v, off);
     }
     __syncthreads();
+    // Each loop reads one LDS row ahead (its eight 16-byte reads in flight while the current
+    // row's 32 FMAs run) and keeps the scheduler from hoisting further (register pressure).
+    // Rows cn .. 31 hold a previous chunk's keys or zeros: their scores are computed and
+    // replaced by -inf, and P.V skips them.
     float x[CH];
     float mx = -INFINITY;
+    float4 rb[8], rn[8];
+    const float* kr = ks + qd * 32;
+#pragma unroll
+    for (int d4 = 0; d4 < 8; ++d4) rb[d4] = *reinterpret_cast<const float4*>(kr + 4 * d4);
 #pragma unroll
     for (int t = 0; t < CH; ++t) {
-      float a = 0.f;
-      if (t < cn) {
+      if (t + 1 < CH) {
 #pragma unroll
-        for (int dd = 0; dd < 32; ++dd)
-          if (qd * 32 + dd < D) a = fmaf(qp[dd], ks[t * LD + qd * 32 + dd], a);
+        for (int d4 = 0; d4 < 8; ++d4) rn[d4] = *reinterpret_cast<const float4*>(kr + (t + 1) * LD + 4 * d4);
+      }
+      float a = 0.f;
+#pragma unroll
+      for (int d4 = 0; d4 < 8; ++d4) {
+        a = fmaf(qp[4 * d4], rb[d4].x, a);
+        a = fmaf(qp[4 * d4 + 1], rb[d4].y, a);
+        a = fmaf(qp[4 * d4 + 2], rb[d4].z, a);
+        a = fmaf(qp[4 * d4 + 3], rb[d4].w, a);
       }
       a = quad_sum(a);
       x[t] = t < cn ? a * c : -INFINITY;
       mx = fmaxf(mx, x[t]);
+#pragma unroll
+      for (int d4 = 0; d4 < 8; ++d4) rb[d4] = rn[d4];
+      __builtin_amdgcn_sched_barrier(0);
     }
     const float mn = fmaxf(m, mx);
     const float al = fast_exp2(m - mn);  // 0 on the first step
     l *= al;
 #pragma unroll
     for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
+    const float* vr = vs + qd * 32;
+#pragma unroll
+    for (int d4 = 0; d4 < 8; ++d4) rb[d4] = *reinterpret_cast<const float4*>(vr + 4 * d4);
 #pragma unroll
     for (int t = 0; t < CH; ++t) {
+      if (t + 1 < CH) {
+#pragma unroll
+        for (int d4 = 0; d4 < 8; ++d4) rn[d4] = *reinterpret_cast<const float4*>(vr + (t + 1) * LD + 4 * d4);
+      }
       if (t < cn) {
         const float p = fast_exp2(x[t] - mn);
         l += p;
         const float pr = EL::round(p);  // P cast to v's type before P.V (:185)
 #pragma unroll
-        for (int dd = 0; dd < 32; ++dd)
-          if (qd * 32 + dd < D) op[dd] = fmaf(pr, vs[t * LD + qd * 32 + dd], op[dd]);
+        for (int d4 = 0; d4 < 8; ++d4) {
+          op[4 * d4] = fmaf(pr, rb[d4].x, op[4 * d4]);
+          op[4 * d4 + 1] = fmaf(pr, rb[d4].y, op[4 * d4 + 1]);
+          op[4 * d4 + 2] = fmaf(pr, rb[d4].z, op[4 * d4 + 2]);
+          op[4 * d4 + 3] = fmaf(pr, rb[d4].w, op[4 * d4 + 3]);
+        }
       }
+#pragma unroll
+      for (int d4 = 0; d4 < 8; ++d4) rb[d4] = rn[d4];
+      __builtin_amdgcn_sched_barrier(0);
     }
     m = mn;
   };
@@ -375,9 +419,15 @@ __global__ __launch_bounds__(256) void k4_sparse_attn_any(
           __syncthreads();
           for (int dr = 0; dr < dn; ++dr) {
             const float qv = qsh[r * LD + d0 + dr];
+            const float4* hr = reinterpret_cast<const float4*>(kv + dr * LD + qd * 32);
 #pragma unroll
-            for (int dd = 0; dd < 32; ++dd)
-              if (qd * 32 + dd < D) rr[dd] = fmaf(qv, kv[dr * LD + qd * 32 + dd], rr[dd]);
+            for (int d4 = 0; d4 < 8; ++d4) {
+              const float4 hh = hr[d4];
+              rr[4 * d4] = fmaf(qv, hh.x, rr[4 * d4]);
+              rr[4 * d4 + 1] = fmaf(qv, hh.y, rr[4 * d4 + 1]);
+              rr[4 * d4 + 2] = fmaf(qv, hh.z, rr[4 * d4 + 2]);
+              rr[4 * d4 + 3] = fmaf(qv, hh.w, rr[4 * d4 + 3]);
+            }
           }
         }
         const float f = ps * scale;
