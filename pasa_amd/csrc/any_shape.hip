@@ -270,22 +270,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int dd = 0; dd < 32; ++dd) op[dd] = 0.f;
   float m = -INFINITY, l = 0.f, gam = 0.f;
 
-  // Keys [key0, key0 + cn), cn <= 32, all valid: one online-softmax step (:174-186).
-  auto chunk = [&](int key0, int cn) __attribute__((always_inline)) {
-    __syncthreads();
-    for (int i = tid; i < cn * D; i += 256) {
-      const int t = i / D;
-      const int d = i - t * D;
-      const int64_t off = sbase + (int64_t)(key0 + t) * D + d;
-      ks[t * LD + d] = EL::load(k, off);
-      vs[t * LD + d] = EL::load(v, off);
-    }
-    __syncthreads();
-    // Each loop reads one LDS row ahead (its eight 16-byte reads in flight while the current
-    // row's 32 FMAs run) and keeps the scheduler from hoisting further (register pressure).
-    // Rows cn .. 31 hold a previous chunk's keys or zeros: their scores are computed and
-    // replaced by -inf, and P.V skips them.
-    float x[CH];
+  // Rows 0 .. 31 of ks / vs against this lane's features.  Each loop reads one LDS row ahead
+  // (its eight 16-byte reads in flight while the current row's 32 FMAs run) and keeps the
+  // scheduler from hoisting further (register pressure).  Rows past the staged ones hold
+  // earlier rows or zeros: their scores are computed and replaced by -inf, and P.V skips them.
+  float x[CH];
+  // x[t] = c q . ks[t] where keep(t), else -inf; returns the max.
+  auto scores = [&](auto keep) __attribute__((always_inline)) -> float {
     float mx = -INFINITY;
     float4 rb[8], rn[8];
     const float* kr = ks + qd * 32;
@@ -306,17 +297,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         a = fmaf(qp[4 * d4 + 3], rb[d4].w, a);
       }
       a = quad_sum(a);
-      x[t] = t < cn ? a * c : -INFINITY;
+      x[t] = keep(t) ? a * c : -INFINITY;
       mx = fmaxf(mx, x[t]);
 #pragma unroll
       for (int d4 = 0; d4 < 8; ++d4) rb[d4] = rn[d4];
       __builtin_amdgcn_sched_barrier(0);
     }
-    const float mn = fmaxf(m, mx);
-    const float al = fast_exp2(m - mn);  // 0 on the first step
-    l *= al;
-#pragma unroll
-    for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
+    return mx;
+  };
+  // For the rows where use(t): p = exp2(x[t] - mn), f(t, p), o += round(p) * vs[t] (P cast to
+  // v's type before P.V, :185).
+  auto pv = [&](float mn, auto use, auto f) __attribute__((always_inline)) {
+    float4 rb[8], rn[8];
     const float* vr = vs + qd * 32;
 #pragma unroll
     for (int d4 = 0; d4 < 8; ++d4) rb[d4] = *reinterpret_cast<const float4*>(vr + 4 * d4);
@@ -326,10 +318,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int d4 = 0; d4 < 8; ++d4) rn[d4] = *reinterpret_cast<const float4*>(vr + (t + 1) * LD + 4 * d4);
       }
-      if (t < cn) {
+      if (use(t)) {
         const float p = fast_exp2(x[t] - mn);
-        l += p;
-        const float pr = EL::round(p);  // P cast to v's type before P.V (:185)
+        f(t, p);
+        const float pr = EL::round(p);
 #pragma unroll
         for (int d4 = 0; d4 < 8; ++d4) {
           op[4 * d4] = fmaf(pr, rb[d4].x, op[4 * d4]);
@@ -342,6 +334,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int d4 = 0; d4 < 8; ++d4) rb[d4] = rn[d4];
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+
+  // Keys [key0, key0 + cn), cn <= 32, all valid: one online-softmax step (:174-186).
+  auto chunk = [&](int key0, int cn) __attribute__((always_inline)) {
+    __syncthreads();
+    for (int i = tid; i < cn * D; i += 256) {
+      const int t = i / D;
+      const int d = i - t * D;
+      const int64_t off = sbase + (int64_t)(key0 + t) * D + d;
+      ks[t * LD + d] = EL::load(k, off);
+      vs[t * LD + d] = EL::load(v, off);
+    }
+    __syncthreads();
+    auto valid = [&](int t) { return t < cn; };
+    const float mn = fmaxf(m, scores(valid));
+    const float al = fast_exp2(m - mn);  // 0 on the first step
+    l *= al;
+#pragma unroll
+    for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
+    pv(mn, valid, [&](int, float p) { l += p; });
     m = mn;
   };
   auto keys = [&](int a, int b) __attribute__((always_inline)) {
@@ -370,12 +382,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float* vcb = vc + (int64_t)bh * NT * D;
       const float* hgb = hgroup + (int64_t)bh * NG * D * D;
       auto selected = [&](int j) { return (mrow[j >> 5] >> (j & 31)) & 1u; };
-      auto sbar = [&](int j) __attribute__((always_inline)) {  // c q . kbar_j, kbar in the input type (:216-217)
-        float a = 0.f;
-#pragma unroll
-        for (int dd = 0; dd < 32; ++dd)
-          if (qd * 32 + dd < D) a = fmaf(qp[dd], EL::round(kcb[(int64_t)j * D + qd * 32 + dd]), a);
-        return quad_sum(a) * c;
+      // kbar and V^ rows jc .. jc + cn - 1 into ks / vs, in the input type (:216-217, :238).
+      auto zstage = [&](int jc, int cn, bool with_v) __attribute__((always_inline)) {
+        __syncthreads();
+        for (int i = tid; i < cn * D; i += 256) {
+          const int t = i / D;
+          const int d = i - t * D;
+          const int64_t off = (int64_t)(jc + t) * D + d;
+          ks[t * LD + d] = EL::round(kcb[off]);
+          if (with_v) vs[t * LD + d] = EL::round(vcb[off]);
+        }
+        __syncthreads();
       };
       for (int g = 0; g < NG; ++g) {
         const int j0 = g * G;
@@ -383,9 +400,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         int napprox = 0;
         for (int j = j0; j < j1; ++j) napprox += selected(j) ? 0 : 1;
         if (napprox == 0) continue;  // nothing approximated: alpha = 1 and no contribution
+        // Zero order over the group's unselected blocks, 32 at a time: the group max first
+        // (a group of at most 32 blocks keeps its scores and rows for the second pass).
+        const bool one = j1 - j0 <= CH;
         float gm = -INFINITY;
-        for (int j = j0; j < j1; ++j)
-          if (!selected(j)) gm = fmaxf(gm, sbar(j));
+        for (int jc = j0; jc < j1; jc += CH) {
+          const int cn = min(CH, j1 - jc);
+          zstage(jc, cn, one);
+          gm = fmaxf(gm, scores([&](int t) { return t < cn && !selected(jc + t); }));
+        }
         const float mn = fmaxf(m, gm);
         const float al = fast_exp2(m - mn);
         l *= al;
@@ -394,15 +417,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
         m = mn;
         float ps = 0.f;
-        for (int j = j0; j < j1; ++j) {
-          if (selected(j)) continue;
-          const float p = fast_exp2(sbar(j) - m);
-          ps += p;
-          gam += p * (float)(j == NT - 1 ? last_len : BT);  // :242-243
-          const float pr = EL::round(p);
-#pragma unroll
-          for (int dd = 0; dd < 32; ++dd)
-            if (qd * 32 + dd < D) op[dd] = fmaf(pr, EL::round(vcb[(int64_t)j * D + qd * 32 + dd]), op[dd]);
+        for (int jc = j0; jc < j1; jc += CH) {
+          const int cn = min(CH, j1 - jc);
+          auto keep = [&](int t) { return t < cn && !selected(jc + t); };
+          if (!one) {
+            zstage(jc, cn, true);
+            scores(keep);
+          }
+          pv(m, keep, [&](int t, float p) {
+            ps += p;
+            gam += p * (float)(jc + t == NT - 1 ? last_len : BT);  // :242-243
+          });
         }
         // First order (:246-253): r = q . Hbar_g (Hbar in q's type), o += r * (sum p * scale).
         float rr[32];
