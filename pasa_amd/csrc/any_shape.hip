@@ -44,9 +44,8 @@ struct F16E {
 };
 
 constexpr int kAnyChunk = 32;   // rows of a staged K/V chunk
-constexpr int kAnyLd = 129;     // LDS row stride (floats) of the statistics kernel's chunks
-constexpr int kAnyLdA = 132;    // ... and of the attention kernel's tiles: 16-byte rows, so a
-                                // lane's 32 features are eight ds_read_b128
+constexpr int kAnyLd = 132;     // LDS row stride (floats) of staged rows: 16-byte aligned, so
+                                // row pieces are ds_read_b128
 constexpr int kAnyTile = 64;    // query rows per attention workgroup
 
 // Sum of x over the four lanes of a row (lanes 4r .. 4r + 3): (x0 + x1) + (x2 + x3) on all
@@ -61,19 +60,23 @@ __device__ __forceinline__ float quad_sum(float x) {
 
 // ---- block statistics ---------------------------------------------------------
 // One workgroup (256 threads) per (group of G key blocks, slice); the group's blocks in
-// ascending order.  Thread t owns the entries i = t + 256 m (m < ceil(D*D / 256)) of the
-// D x D moment, (d, e) = (i / D, i % D): H_j[d][e] = sum_t k_t[d] v_t[e] - kbar_j[d] V^_j[e]
-// (:106-107), accumulated over 32-row chunks staged in LDS.  Threads t < D own column t
-// of the block sums of q, k and v.  The group sum adds H_j in block order, then / G.
+// ascending order, each in 32-row chunks of k and v staged in LDS as fp32 (132-float rows,
+// feature columns D .. 127 zero).  Thread t owns an 8 x 8 tile of the D x D moment, rows
+// d = 8 (t >> 4) .. + 7 and columns e = 8 (t & 15) .. + 7: per staged row, four 16-byte
+// reads feed 64 FMAs.  H_j[d][e] = sum_t k_t[d] v_t[e] - kbar_j[d] V^_j[e] (:106-107), the
+// sum over the block's rows in order; entries past D stay zero and are not stored.  Threads
+// t < D own column t of the block sums of q, k and v.  The group sum adds H_j in block order,
+// then / G.
 template <typename EL>
 __global__ __launch_bounds__(256) void k2_block_stats_any(const void* __restrict__ q, const void* __restrict__ k,
                                                           const void* __restrict__ v, float* __restrict__ qc,
                                                           float* __restrict__ kc, float* __restrict__ vc,
                                                           float* __restrict__ hnorm, float* __restrict__ hgroup,
                                                           int T, int Tslice, int D, int BT, int NT, int G) {
-  constexpr int CH = kAnyChunk, LD = kAnyLd, MMAX = 128 * 128 / 256;
-  __shared__ float ks[CH * LD];
-  __shared__ float vs[CH * LD];
+  constexpr int CH = kAnyChunk, LD = kAnyLd;
+  __shared__ __attribute__((aligned(16))) float ks[CH * LD];
+  __shared__ __attribute__((aligned(16))) float vs[CH * LD];
+  __shared__ float qsm[CH * 128];  // the chunk's q rows (only their column sums are needed)
   __shared__ float kbar[128];
   __shared__ float vhat[128];
   __shared__ float red[4];
@@ -81,53 +84,60 @@ __global__ __launch_bounds__(256) void k2_block_stats_any(const void* __restrict
   const int bh = blockIdx.y;
   const int tid = threadIdx.x;
   const int NG = (NT + G - 1) / G;
-  const int DD = D * D;
   const int64_t base = (int64_t)bh * Tslice * D;
-  // (d, e) of entry m, stepped from m = 0: i advances by 256.
-  const int d0 = tid / D, e0 = tid - (tid / D) * D;
-  const int dstep = 256 / D, estep = 256 - (256 / D) * D;
-  float gacc[MMAX];
+  const int d0 = 8 * (tid >> 4);
+  const int e0 = 8 * (tid & 15);
+  const bool owns = d0 < D && e0 < D;  // the tile holds at least one entry of the moment
+  for (int i = tid; i < CH * LD; i += 256) {
+    ks[i] = 0.f;
+    vs[i] = 0.f;
+  }
+  if (tid < 128) {
+    kbar[tid] = 0.f;
+    vhat[tid] = 0.f;
+  }
+  float gacc[64];
 #pragma unroll
-  for (int m = 0; m < MMAX; ++m) gacc[m] = 0.f;
+  for (int m = 0; m < 64; ++m) gacc[m] = 0.f;
   const int j1 = min(NT, (g + 1) * G);
   for (int j = g * G; j < j1; ++j) {
     const int r0 = j * BT;
     const int n = min(BT, T - r0);
-    float hacc[MMAX];
+    float hacc[64];
 #pragma unroll
-    for (int m = 0; m < MMAX; ++m) hacc[m] = 0.f;
+    for (int m = 0; m < 64; ++m) hacc[m] = 0.f;
     float qs = 0.f, ksum = 0.f, vsum = 0.f;
     for (int c0 = 0; c0 < n; c0 += CH) {
       const int cn = min(CH, n - c0);
-      __syncthreads();  // the previous chunk's reads are done
+      __syncthreads();  // the previous chunk's reads are done (and the zero fill landed)
       for (int i = tid; i < cn * D; i += 256) {
         const int t = i / D;
         const int d = i - t * D;
         const int64_t off = base + (int64_t)(r0 + c0 + t) * D + d;
         ks[t * LD + d] = EL::load(k, off);
         vs[t * LD + d] = EL::load(v, off);
+        qsm[t * 128 + d] = EL::load(q, off);
       }
       __syncthreads();
       if (tid < D) {
         for (int t = 0; t < cn; ++t) {
           ksum += ks[t * LD + tid];
           vsum += vs[t * LD + tid];
-          qs += EL::load(q, base + (int64_t)(r0 + c0 + t) * D + tid);
+          qs += qsm[t * 128 + tid];
         }
       }
-      int d = d0, e = e0;
+      if (owns) {
+        for (int t = 0; t < cn; ++t) {
+          const float4 k0 = *reinterpret_cast<const float4*>(ks + t * LD + d0);
+          const float4 k1 = *reinterpret_cast<const float4*>(ks + t * LD + d0 + 4);
+          const float4 v0 = *reinterpret_cast<const float4*>(vs + t * LD + e0);
+          const float4 v1 = *reinterpret_cast<const float4*>(vs + t * LD + e0 + 4);
+          const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+          const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-      for (int m = 0; m < MMAX; ++m) {
-        if (tid + 256 * m < DD) {
-          float a = 0.f;
-          for (int t = 0; t < cn; ++t) a = fmaf(ks[t * LD + d], vs[t * LD + e], a);
-          hacc[m] += a;
-        }
-        d += dstep;
-        e += estep;
-        if (e >= D) {
-          e -= D;
-          ++d;
+          for (int a = 0; a < 8; ++a)
+#pragma unroll
+            for (int b = 0; b < 8; ++b) hacc[8 * a + b] = fmaf(kk[a], vv[b], hacc[8 * a + b]);
         }
       }
     }
@@ -143,20 +153,15 @@ __global__ __launch_bounds__(256) void k2_block_stats_any(const void* __restrict
     }
     __syncthreads();
     float nsq = 0.f;
-    int d = d0, e = e0;
+    if (owns) {
 #pragma unroll
-    for (int m = 0; m < MMAX; ++m) {
-      if (tid + 256 * m < DD) {
-        const float h = hacc[m] - kbar[d] * vhat[e];  // :107
-        nsq = fmaf(h, h, nsq);
-        gacc[m] += h;
-      }
-      d += dstep;
-      e += estep;
-      if (e >= D) {
-        e -= D;
-        ++d;
-      }
+      for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const float h = hacc[8 * a + b] - kbar[d0 + a] * vhat[e0 + b];  // :107 (zero past D)
+          nsq = fmaf(h, h, nsq);
+          gacc[8 * a + b] += h;
+        }
     }
     nsq = wave_sum(nsq);
     if ((tid & 63) == 0) red[tid >> 6] = nsq;
@@ -164,10 +169,14 @@ __global__ __launch_bounds__(256) void k2_block_stats_any(const void* __restrict
     if (tid == 0) hnorm[(int64_t)bh * NT + j] = sqrt_rn((red[0] + red[1]) + (red[2] + red[3]));  // :110, :287
   }
   // hbar_g = (1/G) sum over the group, the missing blocks of the last group counting as zeros (:294-299).
-  float* hg = hgroup + ((int64_t)bh * NG + g) * DD;
+  if (owns) {
+    float* hg = hgroup + ((int64_t)bh * NG + g) * D * D;
 #pragma unroll
-  for (int m = 0; m < MMAX; ++m)
-    if (tid + 256 * m < DD) hg[tid + 256 * m] = gacc[m] / (float)G;
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        if (d0 + a < D && e0 + b < D) hg[(d0 + a) * D + e0 + b] = gacc[8 * a + b] / (float)G;
+  }
 }
 
 // ---- selection scores -----------------------------------------------------------
@@ -209,7 +218,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float* __restrict__ kc, const float* __restrict__ vc, const float* __restrict__ hgroup,
     const uint32_t* __restrict__ selmask, void* __restrict__ o, float scale, float c, int T, int text,
     int text_valid, int D, int BT, int NT, int G, int NG, int NW, int gamma_literal, int all) {
-  constexpr int CH = kAnyChunk, LD = kAnyLdA, TR = kAnyTile;
+  constexpr int CH = kAnyChunk, LD = kAnyLd, TR = kAnyTile;
   static_assert(2 * CH * LD >= TR * LD, "an Hbar slab of 64 rows fits the K/V chunk buffers");
   static_assert(LD % 4 == 0, "16-byte LDS rows");
   __shared__ __attribute__((aligned(16))) float kv[2 * CH * LD];  // K chunk, V chunk; phase 2: 64 rows of Hbar
