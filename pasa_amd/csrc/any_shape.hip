@@ -14,9 +14,9 @@
 // P and P-bar cast to it before their products, the output store) and not at all for
 // fp32 inputs, so an fp32 call is the reference's mathematics in fp32.
 //
-// Layout of a query tile: 64 rows, four lanes per row (lane & 3 owns features
-// 32 (lane & 3) .. + 31); a row's dot products are reduced over its four lanes with two
-// DPP quad permutations, which give all four lanes the same bits.
+// Layout of a query tile: 64 rows, eight lanes per pair of rows (rows r and r + 32; lane & 7
+// owns features 16 (lane & 7) .. + 15 of both); a row's dot products are reduced over its
+// eight lanes by DPP, which gives all eight lanes the same bits.
 #include "common.h"
 #include "kernels.h"
 
@@ -48,11 +48,13 @@ constexpr int kAnyLd = 132;     // LDS row stride (floats) of staged rows: 16-by
                                 // row pieces are ds_read_b128
 constexpr int kAnyTile = 64;    // query rows per attention workgroup
 
-// Sum of x over the four lanes of a row (lanes 4r .. 4r + 3): (x0 + x1) + (x2 + x3) on all
-// four (addition commutes, so every lane gets the same bits), by two DPP quad permutations.
-__device__ __forceinline__ float quad_sum(float x) {
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));  // lane ^ 1
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));  // lane ^ 2
+// Sum of x over the eight lanes 8r .. 8r + 7: ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)) on
+// all eight (addition commutes, so every lane gets the same bits), by DPP: two quad
+// permutations (lane ^ 1, lane ^ 2), then the half-row mirror (lane 7 - i of the eight).
+__device__ __forceinline__ float oct_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));   // lane ^ 1
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));   // lane ^ 2
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false));  // 7 - i
   return x;
 }
 
@@ -209,9 +211,11 @@ __global__ __launch_bounds__(256) void k3_scores_any(const float* __restrict__ q
 // (not when `all`).  Text tiles attend densely within their segment ([0, seg) for the
 // prompt rows, [seg, T + text) for the padding rows).  Keys go in chunks of 32 staged in
 // LDS, each chunk one online-softmax step (exact: rescaled whenever a row's max rises).
-// Feature columns D .. 127 of every LDS row hold zeros (written once, never overwritten),
-// as do a lane's q features past D, so the dot products run over all 32 features of a lane
-// with no per-feature test: the extra terms are 0 * 0.
+// Lane mapping: eight lanes per pair of rows (rows rp and rp + 32, rp = tid / 8), lane
+// tid & 7 owning features 16 (tid & 7) .. + 15 of both; a 16-byte LDS read of a key row
+// feeds eight FMAs.  Feature columns D .. 127 of every LDS row hold zeros (written once,
+// never overwritten), as do a lane's q features past D, so the dot products run over all
+// 16 features of a lane with no per-feature test: the extra terms are 0 * 0.
 template <typename EL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k4_sparse_attn_any(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
@@ -220,14 +224,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     int text_valid, int D, int BT, int NT, int G, int NG, int NW, int gamma_literal, int all) {
   constexpr int CH = kAnyChunk, LD = kAnyLd, TR = kAnyTile;
   static_assert(2 * CH * LD >= TR * LD, "an Hbar slab of 64 rows fits the K/V chunk buffers");
-  static_assert(LD % 4 == 0, "16-byte LDS rows");
+  static_assert(LD % 4 == 0 && TR == 64, "16-byte LDS rows; two rows per lane, 32 apart");
   __shared__ __attribute__((aligned(16))) float kv[2 * CH * LD];  // K chunk, V chunk; phase 2: 64 rows of Hbar
   __shared__ __attribute__((aligned(16))) float qsh[TR * LD];     // the tile's q rows
   float* ks = kv;
   float* vs = kv + CH * LD;
   const int tid = threadIdx.x;
-  const int r = tid >> 2;
-  const int qd = tid & 3;
+  const int rp = tid >> 3;        // rows rp and rp + 32 of the tile
+  const int f0 = 16 * (tid & 7);  // this lane's first feature
   const int bh = blockIdx.y;
   const int Ttot = T + text;
   const int seg = T + text_valid;
@@ -265,83 +269,104 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   for (int i = tid; i < 2 * CH * LD; i += 256) kv[i] = 0.f;
   __syncthreads();
-  const bool live = r < rows;
-  float qp[32], op[32];
+  float qp[2][16], op[2][16];
 #pragma unroll
-  for (int d4 = 0; d4 < 8; ++d4) {
-    const float4 qq = *reinterpret_cast<const float4*>(qsh + r * LD + qd * 32 + 4 * d4);
-    qp[4 * d4] = qq.x;
-    qp[4 * d4 + 1] = qq.y;
-    qp[4 * d4 + 2] = qq.z;
-    qp[4 * d4 + 3] = qq.w;
-  }
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-  for (int dd = 0; dd < 32; ++dd) op[dd] = 0.f;
-  float m = -INFINITY, l = 0.f, gam = 0.f;
+    for (int d4 = 0; d4 < 4; ++d4) {
+      const float4 qq = *reinterpret_cast<const float4*>(qsh + (rp + 32 * i) * LD + f0 + 4 * d4);
+      qp[i][4 * d4] = qq.x;
+      qp[i][4 * d4 + 1] = qq.y;
+      qp[i][4 * d4 + 2] = qq.z;
+      qp[i][4 * d4 + 3] = qq.w;
+    }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int dd = 0; dd < 16; ++dd) op[i][dd] = 0.f;
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f}, gam[2] = {0.f, 0.f};
 
   // Rows 0 .. 31 of ks / vs against this lane's features.  Each loop reads one LDS row ahead
-  // (its eight 16-byte reads in flight while the current row's 32 FMAs run) and keeps the
+  // (its four 16-byte reads in flight while the current row's 32 FMAs run) and keeps the
   // scheduler from hoisting further (register pressure).  Rows past the staged ones hold
   // earlier rows or zeros: their scores are computed and replaced by -inf, and P.V skips them.
-  float x[CH];
-  // x[t] = c q . ks[t] where keep(t), else -inf; returns the max.
-  auto scores = [&](auto keep) __attribute__((always_inline)) -> float {
-    float mx = -INFINITY;
-    float4 rb[8], rn[8];
-    const float* kr = ks + qd * 32;
+  float x[2][CH];
+  // x[i][t] = c q_i . ks[t] where keep(t), else -inf; mx[i] = the max over t.
+  auto scores = [&](auto keep, float (&mx)[2]) __attribute__((always_inline)) {
+    mx[0] = mx[1] = -INFINITY;
+    float4 rb[4], rn[4];
+    const float* kr = ks + f0;
 #pragma unroll
-    for (int d4 = 0; d4 < 8; ++d4) rb[d4] = *reinterpret_cast<const float4*>(kr + 4 * d4);
+    for (int d4 = 0; d4 < 4; ++d4) rb[d4] = *reinterpret_cast<const float4*>(kr + 4 * d4);
 #pragma unroll
     for (int t = 0; t < CH; ++t) {
       if (t + 1 < CH) {
 #pragma unroll
-        for (int d4 = 0; d4 < 8; ++d4) rn[d4] = *reinterpret_cast<const float4*>(kr + (t + 1) * LD + 4 * d4);
+        for (int d4 = 0; d4 < 4; ++d4) rn[d4] = *reinterpret_cast<const float4*>(kr + (t + 1) * LD + 4 * d4);
       }
-      float a = 0.f;
+      const bool kp = keep(t);
 #pragma unroll
-      for (int d4 = 0; d4 < 8; ++d4) {
-        a = fmaf(qp[4 * d4], rb[d4].x, a);
-        a = fmaf(qp[4 * d4 + 1], rb[d4].y, a);
-        a = fmaf(qp[4 * d4 + 2], rb[d4].z, a);
-        a = fmaf(qp[4 * d4 + 3], rb[d4].w, a);
+      for (int i = 0; i < 2; ++i) {
+        float a = 0.f;
+#pragma unroll
+        for (int d4 = 0; d4 < 4; ++d4) {
+          a = fmaf(qp[i][4 * d4], rb[d4].x, a);
+          a = fmaf(qp[i][4 * d4 + 1], rb[d4].y, a);
+          a = fmaf(qp[i][4 * d4 + 2], rb[d4].z, a);
+          a = fmaf(qp[i][4 * d4 + 3], rb[d4].w, a);
+        }
+        a = oct_sum(a);
+        x[i][t] = kp ? a * c : -INFINITY;
+        mx[i] = fmaxf(mx[i], x[i][t]);
       }
-      a = quad_sum(a);
-      x[t] = keep(t) ? a * c : -INFINITY;
-      mx = fmaxf(mx, x[t]);
 #pragma unroll
-      for (int d4 = 0; d4 < 8; ++d4) rb[d4] = rn[d4];
+      for (int d4 = 0; d4 < 4; ++d4) rb[d4] = rn[d4];
       __builtin_amdgcn_sched_barrier(0);
     }
-    return mx;
   };
-  // For the rows where use(t): p = exp2(x[t] - mn), f(t, p), o += round(p) * vs[t] (P cast to
-  // v's type before P.V, :185).
-  auto pv = [&](float mn, auto use, auto f) __attribute__((always_inline)) {
-    float4 rb[8], rn[8];
-    const float* vr = vs + qd * 32;
+  // For the rows t where use(t): p_i = exp2(x[i][t] - mn[i]), f(t, p_0, p_1),
+  // o_i += round(p_i) * vs[t] (P cast to v's type before P.V, :185).
+  auto pv = [&](const float (&mn)[2], auto use, auto f) __attribute__((always_inline)) {
+    float4 rb[4], rn[4];
+    const float* vr = vs + f0;
 #pragma unroll
-    for (int d4 = 0; d4 < 8; ++d4) rb[d4] = *reinterpret_cast<const float4*>(vr + 4 * d4);
+    for (int d4 = 0; d4 < 4; ++d4) rb[d4] = *reinterpret_cast<const float4*>(vr + 4 * d4);
 #pragma unroll
     for (int t = 0; t < CH; ++t) {
       if (t + 1 < CH) {
 #pragma unroll
-        for (int d4 = 0; d4 < 8; ++d4) rn[d4] = *reinterpret_cast<const float4*>(vr + (t + 1) * LD + 4 * d4);
+        for (int d4 = 0; d4 < 4; ++d4) rn[d4] = *reinterpret_cast<const float4*>(vr + (t + 1) * LD + 4 * d4);
       }
       if (use(t)) {
-        const float p = fast_exp2(x[t] - mn);
-        f(t, p);
-        const float pr = EL::round(p);
+        const float p0 = fast_exp2(x[0][t] - mn[0]);
+        const float p1 = fast_exp2(x[1][t] - mn[1]);
+        f(t, p0, p1);
+        const float pr[2] = {EL::round(p0), EL::round(p1)};
 #pragma unroll
-        for (int d4 = 0; d4 < 8; ++d4) {
-          op[4 * d4] = fmaf(pr, rb[d4].x, op[4 * d4]);
-          op[4 * d4 + 1] = fmaf(pr, rb[d4].y, op[4 * d4 + 1]);
-          op[4 * d4 + 2] = fmaf(pr, rb[d4].z, op[4 * d4 + 2]);
-          op[4 * d4 + 3] = fmaf(pr, rb[d4].w, op[4 * d4 + 3]);
-        }
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int d4 = 0; d4 < 4; ++d4) {
+            op[i][4 * d4] = fmaf(pr[i], rb[d4].x, op[i][4 * d4]);
+            op[i][4 * d4 + 1] = fmaf(pr[i], rb[d4].y, op[i][4 * d4 + 1]);
+            op[i][4 * d4 + 2] = fmaf(pr[i], rb[d4].z, op[i][4 * d4 + 2]);
+            op[i][4 * d4 + 3] = fmaf(pr[i], rb[d4].w, op[i][4 * d4 + 3]);
+          }
       }
 #pragma unroll
-      for (int d4 = 0; d4 < 8; ++d4) rb[d4] = rn[d4];
+      for (int d4 = 0; d4 < 4; ++d4) rb[d4] = rn[d4];
       __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // The running max of row i rises to mn: rescale its accumulators (and Gamma unless literal).
+  auto rescale = [&](const float (&mn)[2], bool with_gamma) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float al = fast_exp2(m[i] - mn[i]);  // 0 on the first step
+      l[i] *= al;
+      if (with_gamma) gam[i] *= al;
+#pragma unroll
+      for (int dd = 0; dd < 16; ++dd) op[i][dd] *= al;
+      m[i] = mn[i];
     }
   };
 
@@ -357,13 +382,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     __syncthreads();
     auto valid = [&](int t) { return t < cn; };
-    const float mn = fmaxf(m, scores(valid));
-    const float al = fast_exp2(m - mn);  // 0 on the first step
-    l *= al;
-#pragma unroll
-    for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
-    pv(mn, valid, [&](int, float p) { l += p; });
-    m = mn;
+    float mx[2];
+    scores(valid, mx);
+    const float mn[2] = {fmaxf(m[0], mx[0]), fmaxf(m[1], mx[1])};
+    rescale(mn, false);
+    pv(mn, valid, [&](int, float p0, float p1) {
+      l[0] += p0;
+      l[1] += p1;
+    });
   };
   auto keys = [&](int a, int b) __attribute__((always_inline)) {
     for (int k0 = a; k0 < b; k0 += CH) chunk(k0, min(CH, b - k0));
@@ -391,6 +417,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float* vcb = vc + (int64_t)bh * NT * D;
       const float* hgb = hgroup + (int64_t)bh * NG * D * D;
       auto selected = [&](int j) { return (mrow[j >> 5] >> (j & 31)) & 1u; };
+      // Bit t set: block jc + t (t < cn) is approximated, i.e. not selected.
+      auto unselected_bits = [&](int jc, int cn) -> uint32_t {
+        const int w = jc >> 5;
+        const int sh = jc & 31;
+        uint32_t sel = mrow[w] >> sh;
+        if (sh != 0 && w + 1 < NW) sel |= mrow[w + 1] << (32 - sh);
+        return ~sel & (cn >= 32 ? 0xffffffffu : (1u << cn) - 1u);
+      };
       // kbar and V^ rows jc .. jc + cn - 1 into ks / vs, in the input type (:216-217, :238).
       auto zstage = [&](int jc, int cn, bool with_v) __attribute__((always_inline)) {
         __syncthreads();
@@ -412,36 +446,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // Zero order over the group's unselected blocks, 32 at a time: the group max first
         // (a group of at most 32 blocks keeps its scores and rows for the second pass).
         const bool one = j1 - j0 <= CH;
-        float gm = -INFINITY;
+        float gm[2] = {-INFINITY, -INFINITY};
         for (int jc = j0; jc < j1; jc += CH) {
           const int cn = min(CH, j1 - jc);
           zstage(jc, cn, one);
-          gm = fmaxf(gm, scores([&](int t) { return t < cn && !selected(jc + t); }));
+          const uint32_t ub = unselected_bits(jc, cn);
+          float mx[2];
+          scores([&](int t) { return ((ub >> t) & 1u) != 0u; }, mx);
+          gm[0] = fmaxf(gm[0], mx[0]);
+          gm[1] = fmaxf(gm[1], mx[1]);
         }
-        const float mn = fmaxf(m, gm);
-        const float al = fast_exp2(m - mn);
-        l *= al;
-        if (!gamma_literal) gam *= al;  // the literal form never rescales Gamma (:231-235)
-#pragma unroll
-        for (int dd = 0; dd < 32; ++dd) op[dd] *= al;
-        m = mn;
-        float ps = 0.f;
+        const float mn[2] = {fmaxf(m[0], gm[0]), fmaxf(m[1], gm[1])};
+        rescale(mn, !gamma_literal);  // the literal form never rescales Gamma (:231-235)
+        float ps[2] = {0.f, 0.f};
         for (int jc = j0; jc < j1; jc += CH) {
           const int cn = min(CH, j1 - jc);
-          auto keep = [&](int t) { return t < cn && !selected(jc + t); };
+          const uint32_t ub = unselected_bits(jc, cn);
+          auto keep = [&](int t) { return ((ub >> t) & 1u) != 0u; };
           if (!one) {
             zstage(jc, cn, true);
-            scores(keep);
+            float mx[2];
+            scores(keep, mx);
           }
-          pv(m, keep, [&](int t, float p) {
-            ps += p;
-            gam += p * (float)(jc + t == NT - 1 ? last_len : BT);  // :242-243
+          pv(mn, keep, [&](int t, float p0, float p1) {
+            const float len = (float)(jc + t == NT - 1 ? last_len : BT);  // :242-243
+            ps[0] += p0;
+            ps[1] += p1;
+            gam[0] += p0 * len;
+            gam[1] += p1 * len;
           });
         }
         // First order (:246-253): r = q . Hbar_g (Hbar in q's type), o += r * (sum p * scale).
-        float rr[32];
+        float rr[2][16];
 #pragma unroll
-        for (int dd = 0; dd < 32; ++dd) rr[dd] = 0.f;
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int dd = 0; dd < 16; ++dd) rr[i][dd] = 0.f;
         for (int d0 = 0; d0 < D; d0 += TR) {
           const int dn = min(TR, D - d0);
           __syncthreads();
@@ -452,33 +492,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
           __syncthreads();
           for (int dr = 0; dr < dn; ++dr) {
-            const float qv = qsh[r * LD + d0 + dr];
-            const float4* hr = reinterpret_cast<const float4*>(kv + dr * LD + qd * 32);
+            const float qv[2] = {qsh[rp * LD + d0 + dr], qsh[(rp + 32) * LD + d0 + dr]};
+            const float4* hr = reinterpret_cast<const float4*>(kv + dr * LD + f0);
 #pragma unroll
-            for (int d4 = 0; d4 < 8; ++d4) {
+            for (int d4 = 0; d4 < 4; ++d4) {
               const float4 hh = hr[d4];
-              rr[4 * d4] = fmaf(qv, hh.x, rr[4 * d4]);
-              rr[4 * d4 + 1] = fmaf(qv, hh.y, rr[4 * d4 + 1]);
-              rr[4 * d4 + 2] = fmaf(qv, hh.z, rr[4 * d4 + 2]);
-              rr[4 * d4 + 3] = fmaf(qv, hh.w, rr[4 * d4 + 3]);
+#pragma unroll
+              for (int i = 0; i < 2; ++i) {
+                rr[i][4 * d4] = fmaf(qv[i], hh.x, rr[i][4 * d4]);
+                rr[i][4 * d4 + 1] = fmaf(qv[i], hh.y, rr[i][4 * d4 + 1]);
+                rr[i][4 * d4 + 2] = fmaf(qv[i], hh.z, rr[i][4 * d4 + 2]);
+                rr[i][4 * d4 + 3] = fmaf(qv[i], hh.w, rr[i][4 * d4 + 3]);
+              }
             }
           }
         }
-        const float f = ps * scale;
 #pragma unroll
-        for (int dd = 0; dd < 32; ++dd) op[dd] = fmaf(rr[dd], f, op[dd]);
+        for (int i = 0; i < 2; ++i) {
+          const float f = ps[i] * scale;
+#pragma unroll
+          for (int dd = 0; dd < 16; ++dd) op[i][dd] = fmaf(rr[i][dd], f, op[i][dd]);
+        }
       }
     }
   } else {
     keys(kbeg, kend);
   }
   // o = A / (L + Gamma) (:258-259), stored in the input type (:262).
-  if (live) {
-    const float den = l + gam;
 #pragma unroll
-    for (int dd = 0; dd < 32; ++dd) {
-      const int e = qd * 32 + dd;
-      if (e < D) EL::store(o, sbase + (int64_t)(row0 + r) * D + e, op[dd] / den);
+  for (int i = 0; i < 2; ++i) {
+    const int r = rp + 32 * i;
+    if (r < rows) {
+      const float den = l[i] + gam[i];
+#pragma unroll
+      for (int dd = 0; dd < 16; ++dd) {
+        const int e = f0 + dd;
+        if (e < D) EL::store(o, sbase + (int64_t)(row0 + r) * D + e, op[i][dd] / den);
+      }
     }
   }
 }
