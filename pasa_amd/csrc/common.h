@@ -211,6 +211,11 @@ struct Bf16 {
   __device__ static __forceinline__ f32x16_t mfma(const vec8& a, const vec8& b, const f32x16_t& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  // D(16x16) += A(16x32) * B(32x16): lane l holds A[l%16][8(l/16) .. +7] and
+  // B[8(l/16) .. +7][l%16]; element i of D is D[4(l/16) + i][l%16].
+  __device__ static __forceinline__ f32x4_t mfma16(const vec8& a, const vec8& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
   __device__ static __forceinline__ uint32_t bits(float x) { return f32_to_bf16_bits(x); }
   __device__ static __forceinline__ void widen8(const uint4& c, float* out) { unpack8(c, out); }
@@ -221,6 +226,9 @@ struct F16 {
   static constexpr uint32_t kOne2 = 0x3C003C00u;
   __device__ static __forceinline__ f32x16_t mfma(const vec8& a, const vec8& b, const f32x16_t& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ f32x4_t mfma16(const vec8& a, const vec8& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -262,6 +270,22 @@ __device__ __forceinline__ float halves_max(float x) {
 __device__ __forceinline__ float halves_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// max / sum of x over the four lanes l % 16 + 16 g (g = 0 .. 3), identical on all four:
+// the 32-lane swap pairs g with g ^ 2, then the 16-lane swap pairs g with g ^ 1, and each
+// step combines the two values in the same order on both lanes of the pair.
+__device__ __forceinline__ float quad16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float quad16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
 // No v_dot2c_f32_bf16 (or other dot instructions) in MFMA kernels: on gfx950 a dot

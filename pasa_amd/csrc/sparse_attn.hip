@@ -11,15 +11,18 @@
 //   Finalize (:258-262): o = A / (L + Gamma).
 //
 // MI355X mapping.  One workgroup = one (slice, query block) of BT rows; one
-// wavefront per 32 query rows.  Everything is computed transposed so that a lane
-// owns one query (lane % 32) and the softmax statistics are per-lane scalars:
-//   S^T[key][q]  = K  * Q^T   (v_mfma_f32_32x32x16_bf16 or _f16, K from LDS, Q in VGPRs)
+// wavefront per 32 query rows.  Everything is computed transposed so that the softmax
+// statistics of a query row stay in the lanes that hold it.  In the D = 64 kernel
+// (k4_sparse_attn) a lane owns one query (lane % 32):
+//   S^T[key][q]  = K  * Q^T   (v_mfma_f32_32x32x16_bf16, K from LDS, Q in VGPRs)
 //   O^T[e][q]   += V^T * P^T   (V^T read from the row-major V tile with
 //                               ds_read_b64_tr_b16, P from the S^T accumulators)
 // The S^T accumulator of a lane holds, per 16-key step s, exactly the 8 keys
 // (16s + 8i' + 4h + j) its P^T B-operand slots need; two transposing LDS reads
 // fetch the matching V^T slots.  Keys of a block are consumed in halves of 64
-// (one online-softmax step each) to bound live accumulators.
+// (one online-softmax step each) to bound live accumulators.  The D = 128 kernel
+// (k4_sparse_attn_dma) runs the same transposed products on the 16x16x32 MFMA, a lane
+// owning two query rows (its lane layout is described at the kernel).
 //
 // Phase 1 walks the selected blocks in ascending block order (the selection
 // bitmask) instead of top-k order: exact online softmax is order-independent up
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
     const uint4 w = make_uint4(E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7]));
     *(uint4*)(part2 + P::KB_OFF + xor_tile_byte(m, cc * 8)) = w;
   }
-  // V^T: feature rows e x 4 chunks of 8 (permuted) tokens of the padded tile.
+  // V^T: feature rows e x 4 chunks of 8 blocks (vt_block_of order), kVtRow bytes per row.
 #pragma unroll
   for (int it = 0; it < D * kGroup / 8 / 256; ++it) {
     const int qi = it * 256 + tid;
@@ -177,12 +180,11 @@ __global__ __launch_bounds__(256) void k4_pack_xor(const float* __restrict__ kc,
     float f[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int m = tok_perm(cc * 8 + i);  // tok_perm is its own inverse
-      const int jj = g * kGroup + m;
+      const int jj = g * kGroup + vt_block_of(cc, i);
       f[i] = jj < NT ? vb[(int64_t)jj * D + e] : 0.f;
     }
     const uint4 w = make_uint4(E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7]));
-    *(uint4*)(part2 + P::VT_OFF + PadTile<kGroup>::chunk_byte(e, cc)) = w;
+    *(uint4*)(part2 + P::VT_OFF + e * kVtRow + cc * 16) = w;
   }
   __syncthreads();
   // Hbar^T: row e, chunk cc holds Hbar[8 cc .. 8 cc + 7][e].
@@ -504,10 +506,21 @@ void k4_sparse_attn(const uint16_t* __restrict__ q, const uint16_t* __restrict__
 //   -> wait V_i -> barrier -> load K_{i+1} -> O += V_i P
 // Each barrier both publishes a landed tile and frees the other buffer, so V_i
 // streams in during S + softmax and K_{i+1} during P.V.
-// Tiles use 256-byte rows with XOR-swizzled 16-byte chunks: K chunk c of row r
-// sits at c ^ (r & 15) (conflict-free MFMA A-operand reads of 16 rows), V chunk
-// c at c ^ 4*(r & 3) (conflict-free transposing reads).  The phase-2 pack image
-// is loaded the same way.
+//
+// The products run on the 16x16x32 MFMA (v_mfma_f32_16x16x32_bf16 / _f16).  Under the
+// chip's power limit it sustains about 11% more FLOP/s than the 32x32x16 form on
+// real-valued operands (1.94 against 1.75 PFLOP/s in a bare MFMA stream, at 1.93
+// against 1.72 GHz): the same work per cycle for less energy.  Lane l of a wave owns
+// query rows l % 16 and 16 + l % 16 of the wave's 32 (query tiles qt = 0, 1), and holds,
+// per 16-key tile kt of S^T = K Q^T, keys 16 kt + 4 (l / 16) + {0..3} of both rows; a
+// row's statistics are reduced over its four lanes l % 16 + 16 g.  For P.V the 8 keys of
+// a 32-key step s a lane holds (tiles 2s and 2s + 1) are its B-operand k-slots as they
+// stand, and two transposing LDS reads fetch the V^T A-operand slots for the same keys.
+//
+// Tiles use 256-byte rows with XOR-swizzled 16-byte chunks: K chunk c of row r sits at
+// c ^ (r & 15) (the A-operand reads of 16 rows by one 16-lane group touch 16 distinct
+// chunks), V chunk c at c ^ 2 (r & 7) (the transposing reads of 32 lanes, rows 8 apart,
+// touch 16 distinct chunks).  The phase-2 pack image is loaded the same way.
 
 // PAIR: two query blocks per workgroup, one wave group (QWAVES waves) each, with
 // their K/V tiles side by side in the K and V buffers.
@@ -521,6 +534,9 @@ struct K4D {
   static constexpr int TILE = BT * 256;                    // bytes of one K or V tile
   static constexpr int VW = 4 / QWAVES;                    // 4-row load slots per wave per 16 rows
   static constexpr int TILE_LOADS = TILE / 1024 / QWAVES;  // 1 KB direct loads per wave per tile
+  static constexpr int KT = BT / 16;                       // 16-key tiles of S per block
+  static constexpr int KS = D / 32;                        // 32-feature k-steps
+  static constexpr int DT = D / 16;                        // 16-feature tiles of O
   using PK = K4DPack<BT>;
   static constexpr int KBUF = QBLOCKS * TILE > PK::HT_BYTES ? QBLOCKS * TILE : PK::HT_BYTES;
   static constexpr int VBUF = QBLOCKS * TILE > PK::PART2 ? QBLOCKS * TILE : PK::PART2;
@@ -529,6 +545,15 @@ struct K4D {
   static_assert(PK::PART2 % (1024 * WAVES) == 0 && PK::HT_BYTES % (1024 * WAVES) == 0, "pack split");
 };
 
+// Byte offset in a V tile of the 8 bytes lane `lane` reads with ds_read_b64_tr_b16 for
+// 16-feature tile dt and key rows row0 + 4 (lane / 16) + {0..3}: row row0 + 4 (lane / 16)
+// + (lane % 16) / 4, features 16 dt + 4 (lane % 4) .. + 3 (chunk 2 dt + (lane % 4) / 2,
+// half lane % 2), the chunk stored at c ^ 2 (row & 7).  row0 is a multiple of 16.
+__device__ __forceinline__ int vtile_tr_byte(int row0, int dt, int lane) {
+  const int r = row0 + 4 * (lane >> 4) + ((lane & 15) >> 2);
+  const int c = 2 * dt + ((lane & 3) >> 1);
+  return r * 256 + ((c ^ (2 * (r & 7))) << 4) + 8 * (lane & 1);
+}
 
 // Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008;
@@ -558,7 +583,9 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   constexpr bool all_tiles = ALL;
   using C = K4D<BT, PAIR>;
   using PK = typename C::PK;
+  using vec8 = typename E::vec8;
   constexpr int D = 128;
+  constexpr int KT = C::KT, KS = C::KS, DT = C::DT;
   // Two distinct LDS objects, so the compiler can tell loads into one from reads of the other.
   __shared__ __attribute__((aligned(1024))) unsigned char Ks[C::KBUF];
   __shared__ __attribute__((aligned(1024))) unsigned char Vs[C::VBUF];
@@ -617,36 +644,46 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     row_limit = T;
   }
 
-  const int h = lane >> 5;
-  const int l32 = lane & 31;
+  const int l16 = lane & 15;  // query row within a 16-row query tile; A-operand row
+  const int g4 = lane >> 4;   // which 8 k-slots of an operand, which 4 rows of a result
   const int Ttot = T + text;
   const int64_t slice = (int64_t)bh * Ttot * D;
-  const int qrow = qrow0 + qw * 32 + l32;
   const bool perm = PERM && slice_permuted(rm, bh);
-  const int qrow_st = perm ? map_row(qrow, rm) : qrow;  // frame-major row of this lane's output
+  // This lane's two query rows (query tiles qt = 0, 1), and the frame-major rows their
+  // output goes to (PERM: q is gathered through the same map).
+  int qrow[2], qrow_st[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    qrow[qt] = qrow0 + qw * 32 + 16 * qt + l16;
+    qrow_st[qt] = perm ? map_row(qrow[qt], rm) : qrow[qt];
+  }
 
   const uint32_t slice_bytes = (uint32_t)Ttot * D * 2u;
   const rsrc_t qr = make_rsrc(q + slice, slice_bytes);
-
-  // PERM: q is frame-major (only k and v are token-major copies); each lane gathers its
-  // own query row through the same map as its output store.
-  const int qrow_ld = perm ? qrow_st : qrow;
-  typename E::vec8 qf[D / 16];
+  // Q as B operands: qf[qt][ks] holds features 32 ks + 8 g4 .. + 7 of row qrow[qt].
+  vec8 qf[2][KS];
 #pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks)
-    qf[ks] = as_vec8<E>(buf_load16(qr, ((uint32_t)qrow_ld * D + ks * 16 + h * 8) * 2u));
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[qt][ks] = as_vec8<E>(buf_load16(qr, ((uint32_t)(perm ? qrow_st[qt] : qrow[qt]) * D + ks * 32 + g4 * 8) * 2u));
   // Complete the Q loads now: vector-memory waits the compiler would place at their
   // first use inside the loop would also wait for the tile loads in flight there.
   wait_vmcnt<0>();
 
-  f32x16_t oacc[D / 32];
+  // O^T accumulators: oacc[dt][qt] element i is feature 16 dt + 4 g4 + i of row qrow[qt].
+  f32x4_t oacc[DT][2];
 #pragma unroll
-  for (int et = 0; et < D / 32; ++et)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[et][r] = 0.f;
-  float l_run = 0.f;
-  float g_run = 0.f;
-  float m_run = -INFINITY;
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) oacc[dt][qt][i] = 0.f;
+  // Running max, row sum and Gamma of the two rows: m is the same on the four lanes of a
+  // row; l and Gamma are this lane's partial sums (its keys), added over the four at the end.
+  float l_run[2] = {0.f, 0.f};
+  float g_run[2] = {0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY};
 
   // The selection row is read-only here: constant address space -> scalar loads,
   // which wait on lgkmcnt and leave the in-flight tile loads alone.
@@ -658,16 +695,16 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
 
   // Direct-load lane constants.  Load (vw, n) of this wave covers tile rows
   // 16n + 4*(qw + QWAVES*vw) + lane/16 of its query block's tile; the lane's 16 bytes
-  // land at chunk lane % 16.
+  // land at chunk lane % 16, so it fetches the logical chunk stored there.
   const int lrow = lane >> 4;
   const int lch = lane & 15;
-  uint32_t k_lane[C::VW];
+  uint32_t k_lane[C::VW], v_lane[C::VW];
 #pragma unroll
   for (int vw = 0; vw < C::VW; ++vw) {
     const int r = 4 * (qw + C::QWAVES * vw) + lrow;  // row mod 16
     k_lane[vw] = (uint32_t)(r * 256 + ((lch ^ r) << 4));
+    v_lane[vw] = (uint32_t)(r * 256 + ((lch ^ (2 * (r & 7))) << 4));
   }
-  const uint32_t v_lane0 = (uint32_t)((4 * qw + lrow) * 256 + ((lch ^ (4 * lrow)) << 4));
 
   const u32x4_t kd = make_rsrc_words(k + slice, slice_bytes);
   const u32x4_t vd = make_rsrc_words(v + slice, slice_bytes);
@@ -692,22 +729,18 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     for (int vw = 0; vw < C::VW; ++vw)
 #pragma unroll
       for (int n = 0; n < BT / 16; ++n)
-        dma_load16_lds(vd, vt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256,
-                       v_lane0 + (4 * C::QWAVES * vw + 16 * n) * 256, soff);
+        dma_load16_lds(vd, vt_lds + (16 * n + 4 * (qw + C::QWAVES * vw)) * 256, v_lane[vw] + 16 * n * 256, soff);
   };
 
-  // MFMA operand addresses: K-layout A fragments (also used for Hbar^T and kbar)
-  // and the transposing V reads.
-  int kofs[D / 16];
+  // MFMA A-operand offsets of K-layout tiles (K, Hbar^T, kbar): row l16 of a 16-row tile,
+  // chunk 4 ks + g4 (features 32 ks + 8 g4 .. + 7), stored at chunk ^ l16.
+  int kofs[KS];
 #pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks) kofs[ks] = l32 * 256 + (((2 * ks + h) ^ (l32 & 15)) << 4);
-  const int g16 = lane >> 4;
-  const int i16 = lane & 15;
-  int vofs[D / 32];
+  for (int ks = 0; ks < KS; ++ks) kofs[ks] = l16 * 256 + (((4 * ks + g4) ^ l16) << 4);
+  // The transposing V reads of 32-key step s: keys 32 s + 16 h2 + 4 g4 + {0..3} (h2 = 0, 1).
+  int vofs[DT];
 #pragma unroll
-  for (int et = 0; et < D / 32; ++et)
-    vofs[et] = (4 * (g16 >> 1) + (i16 >> 2)) * 256 +
-               ((4 * (et ^ (i16 >> 2)) + 2 * (g16 & 1) + ((i16 & 3) >> 1)) << 4) + 8 * (i16 & 1);
+  for (int dt = 0; dt < DT; ++dt) vofs[dt] = vtile_tr_byte(0, dt, lane);
 
   int wsel = 0;
   int jall = 0;
@@ -766,102 +799,121 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     barrier_lds_reads_done();  // ... and every wave's; every wave is done reading the V buffer
     load_v(blk);
 
-    f32x16_t sacc[BT / 32];
+    // S^T = K Q^T: sacc[kt][qt] element i = key 16 kt + 4 g4 + i against row qrow[qt].
+    f32x4_t sacc[KT][2];
 #pragma unroll
-    for (int mt = 0; mt < BT / 32; ++mt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[mt][r] = 0.f;
+      for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
+        for (int i = 0; i < 4; ++i) sacc[kt][qt][i] = 0.f;
 #pragma unroll
-      for (int mt = 0; mt < BT / 32; ++mt) {
-        const typename E::vec8 a = as_vec8<E>(lds_ld<uint4>(Ks + tile_off, kofs[ks] + mt * 32 * 256));
-        sacc[mt] = E::mfma(a, qf[ks], sacc[mt]);
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const vec8 a = as_vec8<E>(lds_ld<uint4>(Ks + tile_off, kofs[ks] + kt * 16 * 256));
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) sacc[kt][qt] = E::mfma16(a, qf[qt][ks], sacc[kt][qt]);
       }
-    // Keep 8 fragment reads in flight: each MFMA consumes a read issued 8 MFMAs
-    // (~256 cycles) earlier, which covers the LDS latency.
+    // Keep 8 fragment reads in flight: each read feeds two MFMAs, consumed ~16 MFMAs
+    // (~256 cycles) after it was issued, which covers the LDS latency.
     {
-      constexpr int N = (D / 16) * (BT / 32);
+      constexpr int NR = KS * KT;
 #pragma unroll
       for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
 #pragma unroll
-      for (int i = 0; i < N - 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      for (int i = 0; i < NR - 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
     }
 
     const int nvalid = nv_cur;
     if (nvalid < BT) {
-      // key mt*32 + 8(r>>2) + 4h + (r&3) is past the tile's rows iff its h-free part
-      // reaches lim; comparing against immediates keeps no per-key constants live.
-      const int lim = nvalid - 4 * h;
+      // key 16 kt + 4 g4 + i is past the tile's rows iff 16 kt + i reaches lim;
+      // comparing against immediates keeps no per-key constants live.
+      const int lim = nvalid - 4 * g4;
 #pragma unroll
-      for (int mt = 0; mt < BT / 32; ++mt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (mt * 32 + 8 * (r >> 2) + (r & 3) >= lim) sacc[mt][r] = -INFINITY;
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kt * 16 + i >= lim) sacc[kt][qt][i] = -INFINITY;
     }
-    float mx = -INFINITY;
+    float mxc[2];
 #pragma unroll
-    for (int mt = 0; mt < BT / 32; ++mt)
+    for (int qt = 0; qt < 2; ++qt) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[mt][r]);
-    const float mxc = halves_max(mx) * c;
-    if (__any(mxc > m_run)) {
-      const float m_new = fmaxf(m_run, mxc);
-      const float alpha = fast_exp2(m_run - m_new);  // 0 on the first block
-      m_run = m_new;
-      l_run *= alpha;
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int et = 0; et < D / 32; ++et)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kt][qt][i]);
+      mxc[qt] = quad16_max(mx) * c;
     }
-    // The row sum adds the fp32 p (as gpa.py:182-184 sums `score` before its bf16
-    // cast) in four partial sums, then adds the tile's sum to the rescaled l.
-    typename E::vec8 pf[BT / 16];
-    float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+    if (__any(mxc[0] > m_run[0] || mxc[1] > m_run[1])) {
 #pragma unroll
-    for (int s = 0; s < BT / 16; ++s) {
-      uint32_t w[4];
+      for (int qt = 0; qt < 2; ++qt) {
+        const float m_new = fmaxf(m_run[qt], mxc[qt]);
+        const float alpha = fast_exp2(m_run[qt] - m_new);  // 0 on the first block, 1 if the max held
+        m_run[qt] = m_new;
+        l_run[qt] *= alpha;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p0 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i], c, -m_run));
-        const float p1 = fast_exp2(fmaf(sacc[s >> 1][8 * (s & 1) + 2 * i + 1], c, -m_run));
-        w[i] = E::pack2(p0, p1);
-        lsum[i] += p0 + p1;
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[dt][qt][i] *= alpha;
       }
-      pf[s] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
     }
-    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+    // P in the B-operand layout of 32-key step s: slots 0-3 = tile 2s, 4-7 = tile 2s + 1.
+    // The row sum adds the fp32 p (as gpa.py:182-184 sums `score` before its bf16
+    // cast), then adds the tile's sum to the rescaled l.
+    vec8 pf[KT / 2][2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float lsum[2] = {0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KT / 2; ++s) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4_t& src = sacc[2 * s + (j >> 1)][qt];
+          const float p0 = fast_exp2(fmaf(src[2 * (j & 1)], c, -m_run[qt]));
+          const float p1 = fast_exp2(fmaf(src[2 * (j & 1) + 1], c, -m_run[qt]));
+          w[j] = E::pack2(p0, p1);
+          lsum[j & 1] += p0 + p1;
+        }
+        pf[s][qt] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
+      }
+      l_run[qt] += lsum[0] + lsum[1];
+    }
     // V_blk is waited for only now, so its load overlaps S and the softmax.
     wait_vmcnt<0>();
     barrier_lds_reads_done();  // every wave's part of V_blk landed; every wave is done reading K_blk
     if (nxt >= 0) load_k(nxt);
 #pragma unroll
-    for (int s = 0; s < BT / 16; ++s)
+    for (int s = 0; s < KT / 2; ++s)
 #pragma unroll
-      for (int et = 0; et < D / 32; ++et) {
-        const uint2 lo = lds_read_tr16(Vs + tile_off, vofs[et] + s * 16 * 256);
-        const uint2 hi = lds_read_tr16(Vs + tile_off, vofs[et] + s * 16 * 256 + 8 * 256);
-        const typename E::vec8 a = as_vec8<E>((u32x4_t){lo.x, lo.y, hi.x, hi.y});
-        oacc[et] = E::mfma(a, pf[s], oacc[et]);
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint2 lo = lds_read_tr16(Vs + tile_off, vofs[dt] + s * 32 * 256);
+        const uint2 hi = lds_read_tr16(Vs + tile_off, vofs[dt] + s * 32 * 256 + 16 * 256);
+        const vec8 a = as_vec8<E>((u32x4_t){lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = E::mfma16(a, pf[s][qt], oacc[dt][qt]);
       }
-    // Same read-ahead for the transposing V reads (two per MFMA): 4 MFMAs of operands in flight.
+    // Read-ahead for the transposing V reads: two per A operand, which feeds two MFMAs.
     {
-      constexpr int N = (BT / 16) * (D / 32);
+      constexpr int NM = (KT / 2) * DT * 2;
 #pragma unroll
       for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 1);
 #pragma unroll
-      for (int i = 0; i < N - 4; ++i) {
+      for (int i = 0; i < NM - 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 1);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+      for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
     }
     blk = nxt;
     nv_cur = nv_nxt;
@@ -877,8 +929,8 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   // ---------------- Phase 2 ------------------------------------------------------
   const int last_len = T - (NT - 1) * BT;
   const u32x4_t pd = make_rsrc_words(pack + (int64_t)bh * NG * PK::BYTES, (uint32_t)(NG * PK::BYTES));
-  const unsigned char* Pvt = Vs + PK::VT_OFF;
-  const int pv_base = PadTile<kGroup>::frag_base(l32, h);
+  // V^T of the group: row 16 dt + l16, chunk g4 (blocks 4 g4 + {0..3}, 16 + 4 g4 + {0..3}).
+  const int pv_base = PK::VT_OFF + l16 * kVtRow + g4 * 16;
   const int ng_run = (dense || all_tiles) ? 0 : NG;  // text rows and dense attention: no correction term
   // Groups with at least one unselected in-range block (of either block of a pair),
   // in ascending order.
@@ -929,95 +981,124 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
     const int gn = next_group(g);
     const uint32_t approx = approx_of(g);
 
-    f32x16_t sb;
+    // s-bar^T = kbar Q^T: sb[bt][qt] element i = block 16 bt + 4 g4 + i of the group.
+    f32x4_t sb[2][2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sb[r] = 0.f;
+    for (int bt = 0; bt < 2; ++bt)
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      const typename E::vec8 a = as_vec8<E>(lds_ld<uint4>(Vs, PK::KB_OFF + kofs[ks]));
-      sb = E::mfma(a, qf[ks], sb);
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sb[bt][qt][i] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt) {
+        const vec8 a = as_vec8<E>(lds_ld<uint4>(Vs, PK::KB_OFF + kofs[ks] + bt * 16 * 256));
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) sb[bt][qt] = E::mfma16(a, qf[qt][ks], sb[bt][qt]);
+      }
+    // Blocks of the group that are selected (or past NT) drop out: element i of sb[bt]
+    // is block 16 bt + 4 g4 + i, so its keep mask is one sign-extended bit of approx >> 4 g4.
+    const uint32_t ah = approx >> (4 * g4);
+    float m_new[2], alpha[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float gmx = -INFINITY;
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe((int)ah, 16 * bt + i, 1);
+          sb[bt][qt][i] = __uint_as_float((__float_as_uint(sb[bt][qt][i]) & keep) | (~keep & 0xff800000u));  // -inf if dropped
+          gmx = fmaxf(gmx, sb[bt][qt][i]);
+        }
+      m_new[qt] = fmaxf(m_run[qt], quad16_max(gmx) * c);
+      alpha[qt] = fast_exp2(m_run[qt] - m_new[qt]);
+      m_run[qt] = m_new[qt];
+      l_run[qt] *= alpha[qt];
+      if (!gamma_literal) g_run[qt] *= alpha[qt];
     }
-    // Blocks of the group that are selected (or past NT) drop out: element r of a lane
-    // in half h holds block mfma32_row(r, h) = 8(r >> 2) + 4h + (r & 3), so its keep
-    // mask is one sign-extended bit of approx >> 4h.
-    const uint32_t ah = approx >> (4 * h);
-    float gmx = -INFINITY;
+    if (__any(alpha[0] != 1.f || alpha[1] != 1.f)) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe((int)ah, 8 * (r >> 2) + (r & 3), 1);
-      sb[r] = __uint_as_float((__float_as_uint(sb[r]) & keep) | (~keep & 0xff800000u));  // -inf if dropped
-      gmx = fmaxf(gmx, sb[r]);
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[dt][qt][i] *= alpha[qt];
     }
-    const float m_new = fmaxf(m_run, halves_max(gmx) * c);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
-    if (!gamma_literal) g_run *= alpha;
-    if (__any(alpha != 1.f)) {
+    float psum[2] = {0.f, 0.f};
+    vec8 pbf[2];
 #pragma unroll
-      for (int et = 0; et < D / 32; ++et)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[et][r] *= alpha;
-    }
-    float psum = 0.f;
-    typename E::vec8 pbf[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int qt = 0; qt < 2; ++qt) {
       uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r0 = 8 * s + 2 * i;
-        const float p0 = fast_exp2(fmaf(sb[r0], c, -m_new));
-        const float p1 = fast_exp2(fmaf(sb[r0 + 1], c, -m_new));
-        psum += p0 + p1;
-        w[i] = E::pack2(p0, p1);
+      for (int j = 0; j < 4; ++j) {
+        const f32x4_t& src = sb[j >> 1][qt];
+        const float p0 = fast_exp2(fmaf(src[2 * (j & 1)], c, -m_new[qt]));
+        const float p1 = fast_exp2(fmaf(src[2 * (j & 1) + 1], c, -m_new[qt]));
+        psum[qt] += p0 + p1;
+        w[j] = E::pack2(p0, p1);
       }
-      pbf[s] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
+      pbf[qt] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
     }
     // Gamma += sum_j p_j * n_j.  Every block holds BT rows except the last one, NT - 1,
     // which holds last_len: BT * sum(p) (exact, BT being a power of two), corrected for
     // that block in the one group holding it.
-    float gsum = psum * (float)BT;
+    float gsum[2] = {psum[0] * (float)BT, psum[1] * (float)BT};
     if (g == NG - 1 && last_len != BT) {
-      const int mm_last = (NT - 1) - g * kGroup;
-      const int r_last = ((mm_last >> 3) << 2) | (mm_last & 3);
-      float sl = sb[0];
+      const int mm_last = (NT - 1) - g * kGroup;  // block 16 bt + 4 g4 + i of the group
+      if (g4 == ((mm_last >> 2) & 3)) {
 #pragma unroll
-      for (int r = 1; r < 16; ++r)
-        if (r == r_last) sl = sb[r];
-      if (h == ((mm_last >> 2) & 1)) gsum += fast_exp2(fmaf(sl, c, -m_new)) * (float)(last_len - BT);
-    }
-    g_run += gsum;
-    psum = halves_sum(psum);
+        for (int qt = 0; qt < 2; ++qt) {
+          float sl = sb[0][qt][0];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+          for (int bt = 0; bt < 2; ++bt)
 #pragma unroll
-      for (int et = 0; et < D / 32; ++et) {
-        const typename E::vec8 a =
-            as_vec8<E>(lds_ld<uint4>(Pvt, pv_base + et * 32 * PadTile<kGroup>::ROW_BYTES + s * 16));
-        oacc[et] = E::mfma(a, pbf[s], oacc[et]);
+            for (int i = 0; i < 4; ++i)
+              if (16 * bt + i == (mm_last & 16) + (mm_last & 3)) sl = sb[bt][qt][i];
+          gsum[qt] += fast_exp2(fmaf(sl, c, -m_new[qt])) * (float)(last_len - BT);
+        }
       }
+    }
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      g_run[qt] += gsum[qt];
+      psum[qt] = quad16_sum(psum[qt]);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const vec8 a = as_vec8<E>(lds_ld<uint4>(Vs, pv_base + dt * 16 * kVtRow));
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = E::mfma16(a, pbf[qt], oacc[dt][qt]);
+    }
     wait_vmcnt<0>();           // this wave's Hbar^T of group g landed (nothing else is in flight)
     barrier_lds_reads_done();  // every wave is done reading part 2 of group g; Hbar^T of g is in place
     if (gn >= 0) load_part2(gn);
 
-    const float f = psum * scale;
-    f32x16_t racc[D / 32];
+    // r^T = Hbar^T Q^T: racc[dt][qt] element i = feature 16 dt + 4 g4 + i of q.Hbar.
+    f32x4_t racc[DT][2];
 #pragma unroll
-    for (int et = 0; et < D / 32; ++et)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) racc[et][r] = 0.f;
+      for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
+        for (int i = 0; i < 4; ++i) racc[dt][qt][i] = 0.f;
 #pragma unroll
-      for (int et = 0; et < D / 32; ++et) {
-        const typename E::vec8 a = as_vec8<E>(lds_ld<uint4>(Ks, kofs[ks] + et * 32 * 256));
-        racc[et] = E::mfma(a, qf[ks], racc[et]);
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const vec8 a = as_vec8<E>(lds_ld<uint4>(Ks, kofs[ks] + dt * 16 * 256));
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) racc[dt][qt] = E::mfma16(a, qf[qt][ks], racc[dt][qt]);
       }
 #pragma unroll
-    for (int et = 0; et < D / 32; ++et)
+    for (int qt = 0; qt < 2; ++qt) {
+      const float f = psum[qt] * scale;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[et][r] = fmaf(racc[et][r], f, oacc[et][r]);
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) oacc[dt][qt][i] = fmaf(racc[dt][qt][i], f, oacc[dt][qt][i]);
+    }
     if (gn >= 0) wait_vmcnt<0>();  // this wave's part 2 of group gn landed
     barrier_lds_reads_done();      // every wave is done reading Hbar^T of g; part 2 of gn is in place
     if (gn >= 0) load_ht(gn);
@@ -1025,19 +1106,19 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
   }
 
   // O = A / (L + Gamma): one correctly rounded reciprocal per row, then products.
-  const float inv = 1.f / (halves_sum(l_run) + halves_sum(g_run));
-  if (store_rows && qrow < row_limit) {
-    uint16_t* orow = o + slice + (int64_t)qrow_st * D;
 #pragma unroll
-    for (int et = 0; et < D / 32; ++et)
+  for (int qt = 0; qt < 2; ++qt) {
+    const float inv = 1.f / (quad16_sum(l_run[qt]) + quad16_sum(g_run[qt]));
+    if (store_rows && qrow[qt] < row_limit) {
+      uint16_t* orow = o + slice + (int64_t)qrow_st[qt] * D;
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int e0 = et * 32 + 8 * rq + 4 * h;
+      for (int dt = 0; dt < DT; ++dt) {
         uint2 w;
-        w.x = E::pack2(oacc[et][4 * rq + 0] * inv, oacc[et][4 * rq + 1] * inv);
-        w.y = E::pack2(oacc[et][4 * rq + 2] * inv, oacc[et][4 * rq + 3] * inv);
-        *(uint2*)(orow + e0) = w;
+        w.x = E::pack2(oacc[dt][qt][0] * inv, oacc[dt][qt][1] * inv);
+        w.y = E::pack2(oacc[dt][qt][2] * inv, oacc[dt][qt][3] * inv);
+        *(uint2*)(orow + dt * 16 + 4 * g4) = w;
       }
+    }
   }
 }
 

@@ -26,19 +26,21 @@ def test_c2_flops_equal_the_mfma_work():
     """c2 at block 128: every (query block, selected block) pair is one 128 x 128 x 128 tile
     of S = QK^T and one of P.V (4 D BT^2 FLOP), and every (query block, group) pair one
     32-block score tile, one P-bar.V-hat and one Q.H-bar product.  K4 issues
-    443,297,280 32x32x16 MFMAs per launch at c2 (rocprofv3 SQ_INSTS_MFMA, every dispatch), each
-    32,768 FLOP: the count below is that number of MFMAs exactly."""
+    886,594,560 16x16x32 MFMAs per launch at c2 (rocprofv3 SQ_INSTS_MFMA, every dispatch), each
+    16,384 FLOP: the count below is that number of MFMAs exactly.  A wave owns 32 query rows,
+    two 16-row tiles; each product is (output tiles of 16 x 16) x (k-steps of 32)."""
     wl = WORKLOADS["c2"]
     BH, D, BT, G = 40, 128, 128, 32
     NT = -(-75600 // BT)
     NS, NG = int(0.1 * NT), -(-NT // G)
     assert (NT, NS, NG) == (591, 59, 19)
-    per_wave_mfma_tile = (BT // 32) * (D // 16) + (D // 32) * (BT // 16)      # S and P.V, 32 query rows
-    per_wave_mfma_group = (D // 16) + (D // 32) * (G // 16) + (D // 32) * (D // 16)  # s-bar, P-bar.V-hat, Q.H-bar
+    qt = 2                                                                   # 16-row query tiles per wave
+    per_wave_mfma_tile = (BT // 16) * qt * (D // 32) + (D // 16) * qt * (BT // 32)   # S and P.V
+    per_wave_mfma_group = (G // 16) * qt * (D // 32) + (D // 16) * qt * (G // 32) + (D // 16) * qt * (D // 32)
     waves = BH * NT * (BT // 32)
     mfma = waves * (NS * per_wave_mfma_tile + NG * per_wave_mfma_group)
-    assert mfma == 443_297_280
-    assert wl.k4_flops(G, NS) == mfma * 32 * 32 * 16 * 2
+    assert mfma == 886_594_560
+    assert wl.k4_flops(G, NS) == mfma * 16 * 16 * 32 * 2
 
 
 def test_c3_text_flops():
