@@ -853,9 +853,11 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kt][qt][i]);
       mxc[qt] = quad16_max(mx) * c;
     }
-    if (__any(mxc[0] > m_run[0] || mxc[1] > m_run[1])) {
+    // One wave-uniform test per query tile: a tile whose 16 rows all kept their max skips
+    // the 32 products of its O (they would multiply by exactly 1).
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < 2; ++qt) {
+      if (__any(mxc[qt] > m_run[qt])) {
         const float m_new = fmaxf(m_run[qt], mxc[qt]);
         const float alpha = fast_exp2(m_run[qt] - m_new);  // 0 on the first block, 1 if the max held
         m_run[qt] = m_new;
@@ -1018,14 +1020,14 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
       l_run[qt] *= alpha[qt];
       if (!gamma_literal) g_run[qt] *= alpha[qt];
     }
-    if (__any(alpha[0] != 1.f || alpha[1] != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+    for (int qt = 0; qt < 2; ++qt)
+      if (__any(alpha[qt] != 1.f)) {
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) oacc[dt][qt][i] *= alpha[qt];
-    }
+      }
     float psum[2] = {0.f, 0.f};
     vec8 pbf[2];
 #pragma unroll
