@@ -236,6 +236,7 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     uint16_t* __restrict__ kt, uint16_t* __restrict__ vt) {
   constexpr int D = 128;
   constexpr int TILE = BT * 256;
+  constexpr bool RQ = BT < 128;  // 256 VGPRs (two workgroups per CU): see qv below
   __shared__ __attribute__((aligned(1024))) unsigned char Kb[2 * TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char Vb[2 * TILE];
   __shared__ float qpart[2][4][D];  // per-wave Q column sums of the last two blocks
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   // are nontemporal (nt): 4-5% faster at c2 and c3 than cached loads, bit-identical.
   const int prow = tid >> 4;
   const int pc = tid & 15;
-  auto load_slot = [&](int buf, int j, int n, uint4& qdst) {
+  auto load_kv = [&](int buf, int j, int n) {
     uint32_t off, soff;
     if (perm) {
       off = st(j * BT + 16 * n + 4 * wave + lrow) * 256u + (t_lane & 255u);
@@ -290,7 +291,13 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     }
     dma_load16_lds_nt(kd, kb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
     dma_load16_lds_nt(vd, vb_lds + buf * TILE + (16 * n + 4 * wave) * 256, off, soff);
+  };
+  auto load_q = [&](int j, int n, uint4& qdst) {
     qdst = buf_load16_nt(qr, (st(j * BT + 16 * n + prow) * D + pc * 8) * 2u);
+  };
+  auto load_slot = [&](int buf, int j, int n, uint4& qdst) {
+    load_kv(buf, j, n);
+    load_q(j, n, qdst);
   };
 
   // Transposing operand reads: lane gets feature 32 ft + l32, tokens 4h + {0..3} (lo)
@@ -323,16 +330,25 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   // j & 1) and are finished after the next block's barrier, so a block costs one
   // workgroup barrier.
   auto finish = [&](int jj, int b, int nn) {
-    if (tid < D) {
-      const float sm = ((qpart[b][0][tid] + qpart[b][1][tid]) + qpart[b][2][tid]) + qpart[b][3][tid];
-      qc[((int64_t)bh * NT + jj) * D + tid] = sm / (float)nn;
-    } else if (tid == D) {
+    // At BT = 64 the thread's addresses are formed here each time from a fresh copy of its
+    // index: kept live across the block loop instead, they are what the compiler spills.
+    int t = tid;
+    if (RQ) asm volatile("" : "+v"(t));
+    if (t < D) {
+      const float sm = ((qpart[b][0][t] + qpart[b][1][t]) + qpart[b][2][t]) + qpart[b][3][t];
+      qc[((int64_t)bh * NT + jj) * D + t] = sm / (float)nn;
+    } else if (t == D) {
       const float sn = ((npart[b][0] + npart[b][1]) + npart[b][2]) + npart[b][3];
       hnorm[(int64_t)bh * NT + jj] = sqrtf(sn);
     }
   };
 
-  uint4 qv[BT / 16], qn[BT / 16];
+  // Q rows of the current block (qv) and of the next (qn).  At BT = 64 (two workgroups per
+  // CU, 256 VGPRs) a second set does not fit beside the accumulators: the next block's rows
+  // land in qv once the column sums have read them (RQ).  At BT = 128 they load into qn
+  // from the start of the block, which is 2-3% faster there.
+  uint4 qv[BT / 16], qn[RQ ? 1 : BT / 16];
+  auto qnext = [&](int n) -> uint4& { return RQ ? qv[n] : qn[RQ ? 0 : n]; };
   if (j0 < j1) {
 #pragma unroll
     for (int n = 0; n < BT / 16; ++n) load_slot(0, j0, n, qv[n]);
@@ -350,8 +366,12 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
     asm volatile("" ::: "memory");
     if (j > j0) finish(j - 1, buf ^ 1, min(BT, T - (j - 1) * BT));
     if (PRE) {
-      load_slot(buf ^ 1, j + 1, 0, qn[0]);
-      load_slot(buf ^ 1, j + 1, 1, qn[1]);
+      load_kv(buf ^ 1, j + 1, 0);
+      load_kv(buf ^ 1, j + 1, 1);
+      if (!RQ) {
+        load_q(j + 1, 0, qnext(0));
+        load_q(j + 1, 1, qnext(1));
+      }
     }
     const unsigned char* Kt = Kb + buf * TILE;
     const unsigned char* Vt = Vb + buf * TILE;
@@ -394,9 +414,31 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
 #pragma unroll
       for (int i = 0; i < 8; ++i) ps[i] += f[i];
     }
+    // The four 16-lane rows of the wave hold the same chunks: add them with the swaps.  At
+    // BT = 64 this runs before the MFMA steps, so that the sums are not live through them.
+    auto store_qsum = [&]() {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x = ps[i];
+        {
+          const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+          x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        ps[i] = halves_sum(x);
+      }
+      if (lane < 16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qpart[buf][wave][lane * 8 + i] = ps[i];
+      }
+    };
+    if (RQ) store_qsum();
+    if (PRE && RQ) {
+      load_q(j + 1, 0, qnext(0));
+      load_q(j + 1, 1, qnext(1));
+    }
 #pragma unroll
     for (int s2 = 0; s2 < BT / 16; ++s2) {
-      if (PRE && s2 + 2 < BT / 16) load_slot(buf ^ 1, j + 1, s2 + 2, qn[s2 + 2]);
+      if (PRE && s2 + 2 < BT / 16) load_slot(buf ^ 1, j + 1, s2 + 2, qnext(s2 + 2));
       typename E::vec8 af[2], bfr[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) af[mt] = frag(Kt, kofs[mt], s2);
@@ -411,20 +453,7 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) av[nt] = E::mfma(ones, bfr[nt], av[nt]);
     }
-    // The four 16-lane rows of the wave hold the same chunks: add them with the swaps.
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float x = ps[i];
-      {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-      }
-      ps[i] = halves_sum(x);
-    }
-    if (lane < 16) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qpart[buf][wave][lane * 8 + i] = ps[i];
-    }
+    if (!RQ) store_qsum();
     // Means: sum / n, a product by the exact reciprocal when n is a power of two (every
     // full block), else the correctly rounded division.
     const float nf = (float)n;
@@ -467,8 +496,10 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
         }
     const float nsum = wave_sum_xor((nrm[0] + nrm[1]) + (nrm[2] + nrm[3]));
     if (lane == 0) npart[buf][wave] = nsum;
+    if (!RQ) {
 #pragma unroll
-    for (int p = 0; p < BT / 16; ++p) qv[p] = qn[p];
+      for (int p = 0; p < BT / 16; ++p) qv[p] = qnext(p);
+    }
   };
   for (int j = j0; j < j1; ++j) {
     if (j + 1 < j1)
@@ -500,14 +531,18 @@ __global__ __launch_bounds__(256, 128 / BT) void k2_block_stats_dma(
   float* hg = split == 1 ? hgroup + ((int64_t)bh * NG + g) * D * D
                          : partials + (((int64_t)bh * NG + g) * split + part) * D * D;
   const float Gf = split == 1 ? (float)G : 1.0f;
+  int t = tid;  // at BT = 64 the lane's indices formed afresh, not kept live through the block loop
+  if (RQ) asm volatile("" : "+v"(t));
+  const int hx = (t >> 5) & 1;
+  const int lx = t & 31;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const int e = eq + nt * 32 + l32;
+      const int e = eq + nt * 32 + lx;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int d = dq + mt * 32 + mfma32_row(r, h);
+        const int d = dq + mt * 32 + mfma32_row(r, hx);
         hg[d * D + e] = split == 1 ? gacc[mt][nt][r] / Gf : gacc[mt][nt][r];
       }
     }

@@ -1028,7 +1028,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
 #pragma unroll
           for (int i = 0; i < 4; ++i) oacc[dt][qt][i] *= alpha[qt];
       }
-    float psum[2] = {0.f, 0.f};
+    float psum[2];
     vec8 pbf[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -1038,7 +1038,7 @@ void k4_sparse_attn_dma(const uint16_t* __restrict__ q, const uint16_t* __restri
         const f32x4_t& src = sb[j >> 1][qt];
         const float p0 = fast_exp2(fmaf(src[2 * (j & 1)], c, -m_new[qt]));
         const float p1 = fast_exp2(fmaf(src[2 * (j & 1) + 1], c, -m_new[qt]));
-        psum[qt] += p0 + p1;
+        psum[qt] = j == 0 ? p0 + p1 : psum[qt] + (p0 + p1);  // no 0 + x: x may be -0
         w[j] = E::pack2(p0, p1);
       }
       pbf[qt] = as_vec8<E>((u32x4_t){w[0], w[1], w[2], w[3]});
