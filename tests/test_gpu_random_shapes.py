@@ -53,7 +53,7 @@ def draw_cases(seed: int, n: int, tuned_only: bool):
 
 # Plus an empty prompt (text_valid 0: every text row is padding) on each route, which the draw
 # does not reach.
-CASES = (draw_cases(20261202, 16, tuned_only=True) + draw_cases(20261203, 16, tuned_only=False)
+CASES = (draw_cases(20261202, 48, tuned_only=True) + draw_cases(20261203, 24, tuned_only=False)
          + [(1, 1500, 128, 64, 32, "bf16", 0.15, "literal", 100, 0),
             (2, 1300, 128, 128, 32, "f16", 0.25, "consistent", 130, 0),
             (1, 900, 96, 32, 16, "f32", 0.2, "literal", 70, 0)])
